@@ -1,0 +1,114 @@
+"""ctypes binding of libffmoe.so (the C ABI declared in include/ffmoe.h).
+
+The library is built in-tree by ``flashfusedmoe_amd.build``.  There is no
+fallback: if it is missing or fails to load, every entry point raises.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libffmoe.so")
+
+# constants mirrored from include/ffmoe.h
+ROW_DROPPED = -1
+ROW_ALIAS0 = -2
+GATING = {"softmax": 0, "sigmoid": 1}
+ACTIVATION = {"swiglu": 0, "geglu": 1, "relu_squared": 2}
+MAX_EXPERTS = 256
+MAX_TOPK = 16
+STAT_AUX, STAT_Z, STAT_IMBALANCE, STAT_DROP_FRAC, NUM_STATS = 0, 1, 2, 3, 4
+ISTAT_MAX, ISTAT_MIN, ISTAT_DROPPED, NUM_ISTATS = 0, 1, 2, 4
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "ffmoe_last_error": (ctypes.c_char_p, []),
+    "ffmoe_version": (_I, []),
+    "ffmoe_route_workspace_bytes": (ctypes.c_size_t, [_L, _I, _I]),
+    "ffmoe_route_fwd": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "ffmoe_route_scan": (_I, [_L, _I, _I, _I, _I, _F, _F, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "ffmoe_permute": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "ffmoe_gemm_tile_rows": (_I, []),
+    "ffmoe_set_lds_transpose": (_I, [_I]),
+    "ffmoe_gemm_up_glu": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _P, _P]),
+    "ffmoe_gemm_down": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _P, _P]),
+    "ffmoe_gemm_dgrad_glu": (_I, [_P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _P]),
+    "ffmoe_gemm_dgrad": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _P, _P]),
+    "ffmoe_gemm_wgrad": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
+    "ffmoe_combine": (_I, [_P, _P, _P, _P, _L, _I, _I, _P, _P]),
+    "ffmoe_route_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I,
+                             _I, _I, _P, _P, _P, _P]),
+    "ffmoe_glu_fwd": (_I, [_P, _L, _I, _I, _P, _P]),
+    "ffmoe_glu_bwd": (_I, [_P, _P, _L, _I, _I, _P, _P]),
+    "ffmoe_scatter_rows": (_I, [_P, _P, _P, _L, _I, _I, _L, _P, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class FFMoEError(RuntimeError):
+    """A libffmoe entry point rejected its arguments or failed to launch."""
+
+
+def load():
+    """Loads libffmoe.so once and binds every entry point of include/ffmoe.h."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m flashfusedmoe_amd.build` "
+                "(the fused MoE path has no non-HIP fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_ptr(device=None):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def call(name, *args):
+    """Calls an entry point and raises FFMoEError with the library's message
+    when it returns nonzero."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.ffmoe_last_error().decode(errors="replace")
+        raise FFMoEError(f"{name} failed: {msg}")
+    return rc
+
+
+def gemm_tile_rows():
+    return load().ffmoe_gemm_tile_rows()
+
+
+def route_workspace_bytes(N, E, k):
+    return int(load().ffmoe_route_workspace_bytes(N, E, k))
+
+
+def set_lds_transpose(enable):
+    return load().ffmoe_set_lds_transpose(1 if enable else 0)

@@ -1,0 +1,108 @@
+// Shared device helpers for the ffmoe HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/ffmoe.h"
+
+namespace ffmoe {
+
+typedef uint16_t bf16_t;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// Records `msg` as this thread's last error and returns 1.
+int set_error(const std::string& msg);
+// Clears the last error and returns 0.
+int clear_error();
+// Checks hipGetLastError() after a launch; returns 0 or records the failure.
+int check_launch(const char* what);
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet), the rounding torch
+// uses for .to(torch.bfloat16).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Unpack 8 bf16 held in a uint4 (16 bytes) to fp32.
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = static_cast<uint32_t>(f32_to_bf16(f[2 * i])) |
+           (static_cast<uint32_t>(f32_to_bf16(f[2 * i + 1])) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// GLU activations in fp32 (the reference computes them in fp32 from bf16
+// operands, activations.py:27-142).  tanh is taken as 2*sigmoid(2z) - 1
+// (activations.py:21-24).
+__device__ __forceinline__ float glu_fwd(int act, float g, float u) {
+  if (act == FFMOE_ACT_SWIGLU) {
+    return g * (1.0f / (1.0f + expf(-g))) * u;
+  } else if (act == FFMOE_ACT_GEGLU) {
+    const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    const float th = 2.0f / (1.0f + expf(-2.0f * inner)) - 1.0f;
+    return 0.5f * g * (1.0f + th) * u;
+  } else {
+    const float r = g > 0.0f ? g : 0.0f;
+    return r * r * u;
+  }
+}
+
+// d(act)/d(gate), d(act)/d(up) scaled by the upstream grad `ga`.
+__device__ __forceinline__ void glu_bwd(int act, float ga, float g, float u, float* gg,
+                                        float* gu) {
+  if (act == FFMOE_ACT_SWIGLU) {
+    const float s = 1.0f / (1.0f + expf(-g));
+    *gu = ga * g * s;
+    *gg = ga * u * (s * (1.0f + g * (1.0f - s)));
+  } else if (act == FFMOE_ACT_GEGLU) {
+    const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    const float th = 2.0f / (1.0f + expf(-2.0f * inner)) - 1.0f;
+    const float gelu = 0.5f * g * (1.0f + th);
+    const float dinner = 0.7978845608028654f * (1.0f + 3.0f * 0.044715f * g * g);
+    const float dgelu = 0.5f * (1.0f + th) + 0.5f * g * (1.0f - th * th) * dinner;
+    *gu = ga * gelu;
+    *gg = ga * u * dgelu;
+  } else {
+    const float r = g > 0.0f ? g : 0.0f;
+    *gu = ga * r * r;
+    *gg = ga * u * 2.0f * r;
+  }
+}
+
+}  // namespace ffmoe

@@ -1,0 +1,487 @@
+// Routing forward: gate GEMM (MFMA) + scoring + top-k + per-block statistics,
+// the global prefix scan, and the stable permutation into expert-sorted rows.
+//
+// Determinism: every count and rank comes from ordered scans (no atomics), so
+// the permutation equals the reference's stable argsort (fused_moe.py:345)
+// bit for bit, and every fp32 reduction has a fixed order.
+#include <algorithm>
+#include <string>
+
+#include "common.h"
+
+namespace ffmoe {
+
+constexpr int kRouteTokens = 64;   // tokens per route block (4 waves x 16)
+constexpr int kRouteThreads = 256;
+
+struct RouteWs {
+  int32_t* hist;    // [nblk][E] per-block counts, replaced by block bases
+  float* psum;      // [nblk][E] sum of routing weights per expert
+  float* ssum;      // [nblk][E] sum of sigmoid(logit) per expert
+  float* zpart;     // [nblk] sum of lse^2
+};
+
+static inline int64_t route_blocks(int64_t N) { return (N + kRouteTokens - 1) / kRouteTokens; }
+
+static inline RouteWs route_ws(void* ws, int64_t N, int E) {
+  const int64_t nb = route_blocks(N);
+  char* p = static_cast<char*>(ws);
+  RouteWs w;
+  w.hist = reinterpret_cast<int32_t*>(p);
+  p += nb * E * 4;
+  w.psum = reinterpret_cast<float*>(p);
+  p += nb * E * 4;
+  w.ssum = reinterpret_cast<float*>(p);
+  p += nb * E * 4;
+  w.zpart = reinterpret_cast<float*>(p);
+  return w;
+}
+
+// Top-k insertion: keeps the KMAX best (value desc, index asc) seen so far.
+// Scanning experts in ascending order with a strict '>' keeps the lower index
+// ahead on ties, which is the reference's k-round argmax with
+// tie_break_left=True (fused_topk.py:63-70).
+template <int KMAX>
+struct TopK {
+  float v[KMAX];
+  int i[KMAX];
+  __device__ void init() {
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+      v[s] = 0.0f;
+      i[s] = -1;
+    }
+  }
+  __device__ void push(float val, int idx, int k) {
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+      if (s < k) {
+        const bool take = (i[s] < 0) || (val > v[s]);
+        if (take) {
+          const float tv = v[s];
+          const int ti = i[s];
+          v[s] = val;
+          i[s] = idx;
+          val = tv;
+          idx = ti;
+          if (idx < 0) break;
+        }
+      }
+    }
+  }
+};
+
+template <int ET, int KMAX, bool FROM_LOGITS>
+__global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ gate,
+    const bf16_t* __restrict__ logits_in, const float* __restrict__ bias, int64_t N, int D,
+    int E, int k, int gating, int need_ssum, bf16_t* __restrict__ logits_out,
+    int64_t* __restrict__ topk_idx, float* __restrict__ topk_w, float* __restrict__ lse_out,
+    int32_t* __restrict__ rank_local, RouteWs ws) {
+  constexpr int EP = ET * 16;        // padded expert count
+  constexpr int LS = EP + 2;         // LDS row stride (bf16 elements)
+  extern __shared__ float smem[];
+  bf16_t* L = reinterpret_cast<bf16_t*>(smem);       // [64][LS] bf16 logits
+  int* sel_i = reinterpret_cast<int*>(smem + kRouteTokens * LS / 2);  // [64*k]
+  float* sel_w = reinterpret_cast<float*>(sel_i + kRouteTokens * k);  // [64*k]
+  float* zl = sel_w + kRouteTokens * k;              // [64]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t blk = blockIdx.x;
+  const int64_t tok_base = blk * kRouteTokens;
+  const int ntok = static_cast<int>(min<int64_t>(kRouteTokens, N - tok_base));
+
+  if constexpr (FROM_LOGITS) {
+    for (int p = tid; p < kRouteTokens * EP; p += kRouteThreads) {
+      const int t = p / EP, e = p % EP;
+      bf16_t v = 0;
+      if (t < ntok && e < E) v = logits_in[(tok_base + t) * E + e];
+      L[t * LS + e] = v;
+    }
+  } else {
+    // Wave `wave` computes logits of tokens [16*wave, 16*wave+16) against all
+    // experts with v_mfma_f32_16x16x32_bf16: A = x rows (K-contiguous),
+    // B = gate rows (K-contiguous).  Lane l holds row l%16, k-block l/16.
+    f32x4_t acc[ET];
+#pragma unroll
+    for (int t = 0; t < ET; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int row = 16 * wave + (lane & 15);
+    const bool row_ok = row < ntok;
+    const bf16_t* xr = x + (tok_base + (row_ok ? row : 0)) * static_cast<int64_t>(D);
+    const int kq = (lane >> 4) * 8;
+    for (int k0 = 0; k0 < D; k0 += 32) {
+      const int kk = k0 + kq;
+      uint4 av = make_uint4(0, 0, 0, 0);
+      if (row_ok && kk < D) av = *reinterpret_cast<const uint4*>(xr + kk);
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
+#pragma unroll
+      for (int t = 0; t < ET; ++t) {
+        const int e = 16 * t + (lane & 15);
+        uint4 bv = make_uint4(0, 0, 0, 0);
+        if (e < E && kk < D) bv = *reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(e) * D + kk);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv),
+                                                        acc[t], 0, 0, 0);
+      }
+    }
+    // Output layout: lane l holds expert 16t + l%16 for tokens 4*(l/16) + r.
+#pragma unroll
+    for (int t = 0; t < ET; ++t) {
+      const int e = 16 * t + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tl = 16 * wave + 4 * (lane >> 4) + r;
+        const bf16_t h = f32_to_bf16(acc[t][r]);
+        L[tl * LS + e] = h;
+        if (logits_out != nullptr && tl < ntok && e < E)
+          logits_out[(tok_base + tl) * E + e] = h;
+      }
+    }
+  }
+  __syncthreads();
+
+  // One thread per token: scores, top-k, weights, logsumexp.
+  if (tid < kRouteTokens) {
+    const int t = tid;
+    float lse = 0.0f;
+    if (t < ntok) {
+      const bf16_t* lr = L + t * LS;
+      TopK<KMAX> tk;
+      tk.init();
+      float m = -INFINITY, s = 0.0f;
+      for (int e = 0; e < E; ++e) {
+        const float l = bf16_to_f32(lr[e]);
+        float sc = (gating == FFMOE_GATING_SOFTMAX) ? l : 1.0f / (1.0f + expf(-l));
+        if (bias != nullptr) sc += bias[e];
+        tk.push(sc, e, k);
+        if (l > m) {
+          s = s * expf(m - l) + 1.0f;
+          m = l;
+        } else {
+          s += expf(l - m);
+        }
+      }
+      lse = m + logf(s);
+      float w[KMAX];
+      float wsum = 0.0f;
+      if (gating == FFMOE_GATING_SOFTMAX) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < KMAX; ++q)
+          if (q < k) mx = fmaxf(mx, bf16_to_f32(lr[tk.i[q]]));
+#pragma unroll
+        for (int q = 0; q < KMAX; ++q) {
+          if (q < k) {
+            w[q] = expf(bf16_to_f32(lr[tk.i[q]]) - mx);
+            wsum += w[q];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < KMAX; ++q)
+          if (q < k) w[q] = w[q] / wsum;
+      } else {
+#pragma unroll
+        for (int q = 0; q < KMAX; ++q) {
+          if (q < k) {
+            w[q] = 1.0f / (1.0f + expf(-bf16_to_f32(lr[tk.i[q]])));
+            wsum += w[q];
+          }
+        }
+        wsum += 1e-6f;
+#pragma unroll
+        for (int q = 0; q < KMAX; ++q)
+          if (q < k) w[q] = w[q] / wsum;
+      }
+      const int64_t n = tok_base + t;
+#pragma unroll
+      for (int q = 0; q < KMAX; ++q) {
+        if (q < k) {
+          topk_idx[n * k + q] = tk.i[q];
+          topk_w[n * k + q] = w[q];
+          sel_i[t * k + q] = tk.i[q];
+          sel_w[t * k + q] = w[q];
+        }
+      }
+      if (lse_out != nullptr) lse_out[n] = lse;
+    }
+    zl[t] = (t < ntok) ? lse * lse : 0.0f;
+  }
+  __syncthreads();
+
+  // One thread per expert: block-local stable ranks (ascending j), counts,
+  // weight sums and sigmoid sums, all in a fixed order.
+  const int nent = ntok * k;
+  for (int e = tid; e < E; e += kRouteThreads) {
+    int cnt = 0;
+    float ps = 0.0f;
+    for (int j = 0; j < nent; ++j) {
+      if (sel_i[j] == e) {
+        rank_local[tok_base * k + j] = cnt++;
+        ps += sel_w[j];
+      }
+    }
+    ws.hist[blk * E + e] = cnt;
+    ws.psum[blk * E + e] = ps;
+    if (need_ssum) {
+      float ss = 0.0f;
+      for (int t = 0; t < ntok; ++t) ss += 1.0f / (1.0f + expf(-bf16_to_f32(L[t * LS + e])));
+      ws.ssum[blk * E + e] = ss;
+    }
+  }
+  if (tid == 0) {
+    float z = 0.0f;
+    for (int t = 0; t < kRouteTokens; ++t) z += zl[t];
+    ws.zpart[blk] = z;
+  }
+}
+
+// Single block: per-expert prefix over route blocks (block bases replace the
+// histogram in place), counts, row offsets, GEMM tile offsets, losses and
+// routing metrics.
+__global__ __launch_bounds__(256) void route_scan_kernel(
+    int64_t N, int64_t nblk, int E, int k, int mt, int bm, float aux_coeff, float z_coeff,
+    int gating, RouteWs ws, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ tile_offsets, float* __restrict__ stats, int32_t* __restrict__ istats) {
+  __shared__ int s_rows[FFMOE_MAX_EXPERTS];
+  __shared__ int s_tiles[FFMOE_MAX_EXPERTS];
+  __shared__ int s_cnt[FFMOE_MAX_EXPERTS];
+  __shared__ float s_fp[FFMOE_MAX_EXPERTS];
+  const int e = threadIdx.x;
+  if (e < E) {
+    int run = 0;
+    float ps = 0.0f, ss = 0.0f;
+    for (int64_t b = 0; b < nblk; ++b) {
+      const int c = ws.hist[b * E + e];
+      ws.hist[b * E + e] = run;
+      run += c;
+      ps += ws.psum[b * E + e];
+      if (gating == FFMOE_GATING_SIGMOID) ss += ws.ssum[b * E + e];
+    }
+    counts[e] = run;
+    s_cnt[e] = run;
+    const int rows = min(run, mt);
+    s_rows[e] = rows;
+    s_tiles[e] = (rows + bm - 1) / bm;
+    const float P = (gating == FFMOE_GATING_SOFTMAX ? ps : ss) / static_cast<float>(N);
+    s_fp[e] = (static_cast<float>(run) / static_cast<float>(N)) * P;
+  }
+  __syncthreads();
+  if (e == 0) {
+    int ro = 0, to = 0, mx = 0, mn = 0x7fffffff, dropped = 0;
+    int64_t tot = 0;
+    float fp = 0.0f;
+    for (int q = 0; q < E; ++q) {
+      offsets[q] = ro;
+      tile_offsets[q] = to;
+      ro += s_rows[q];
+      to += s_tiles[q];
+      mx = max(mx, s_cnt[q]);
+      mn = min(mn, s_cnt[q]);
+      dropped += s_cnt[q] - s_rows[q];
+      tot += s_cnt[q];
+      fp += s_fp[q];
+    }
+    offsets[E] = ro;
+    tile_offsets[E] = to;
+    float z = 0.0f;
+    for (int64_t b = 0; b < nblk; ++b) z += ws.zpart[b];
+    stats[FFMOE_STAT_AUX] = aux_coeff * static_cast<float>(E) * fp;
+    stats[FFMOE_STAT_Z] = z_coeff * (z / static_cast<float>(N));
+    const float mean = static_cast<float>(tot) / static_cast<float>(E);
+    stats[FFMOE_STAT_IMBALANCE] = static_cast<float>(mx) / (mean + 1e-6f);
+    stats[FFMOE_STAT_DROP_FRAC] = static_cast<float>(dropped) / static_cast<float>(N * k);
+    istats[FFMOE_ISTAT_MAX] = mx;
+    istats[FFMOE_ISTAT_MIN] = mn;
+    istats[FFMOE_ISTAT_DROPPED] = dropped;
+    istats[3] = 0;
+  }
+}
+
+constexpr int kPermTokens = 8;  // tokens per permute block
+
+// Resolves each entry's row (block base + block-local rank), renormalises the
+// kept weights in capacity mode, and copies each token row once from HBM to
+// each of its k destination rows.
+__global__ __launch_bounds__(256) void permute_kernel(
+    const bf16_t* __restrict__ x, const int64_t* __restrict__ topk_idx, float* __restrict__ topk_w,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ rank_local, const int32_t* __restrict__ base, int64_t N, int D,
+    int E, int k, int mt, int capacity_mode, bf16_t* __restrict__ xs, int32_t* __restrict__ row_of) {
+  __shared__ int s_row[kPermTokens * FFMOE_MAX_TOPK];
+  const int tid = threadIdx.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kPermTokens;
+  const int ntok = static_cast<int>(min<int64_t>(kPermTokens, N - t0));
+  const int nent = ntok * k;
+  for (int q = tid; q < nent; q += blockDim.x) {
+    const int64_t j = t0 * k + q;
+    const int64_t n = j / k;
+    const int e = static_cast<int>(topk_idx[j]);
+    const int rank = base[(n / kRouteTokens) * E + e] + rank_local[j];
+    int row;
+    if (rank < mt) {
+      row = offsets[e] + rank;
+    } else if (capacity_mode) {
+      row = FFMOE_ROW_DROPPED;
+    } else {
+      row = counts[0] > 0 ? FFMOE_ROW_ALIAS0 : FFMOE_ROW_DROPPED;
+    }
+    s_row[q] = row;
+    row_of[j] = row;
+  }
+  __syncthreads();
+  if (capacity_mode && tid < ntok) {
+    // fused_moe.py:371-375: w*keep / (sum + (1 - has_any))
+    const int64_t n = t0 + tid;
+    float s = 0.0f;
+    for (int q = 0; q < k; ++q) {
+      const float w = s_row[tid * k + q] >= 0 ? topk_w[n * k + q] : 0.0f;
+      s += w;
+    }
+    const float den = s + (s > 0.0f ? 0.0f : 1.0f);
+    for (int q = 0; q < k; ++q) {
+      const float w = s_row[tid * k + q] >= 0 ? topk_w[n * k + q] : 0.0f;
+      topk_w[n * k + q] = w / den;
+    }
+  }
+  const int nvec = D / 8;
+  for (int p = tid; p < ntok * nvec; p += blockDim.x) {
+    const int t = p / nvec, v = p % nvec;
+    const uint4 val = reinterpret_cast<const uint4*>(x + (t0 + t) * static_cast<int64_t>(D))[v];
+    for (int q = 0; q < k; ++q) {
+      const int row = s_row[t * k + q];
+      if (row >= 0) reinterpret_cast<uint4*>(xs + static_cast<int64_t>(row) * D)[v] = val;
+    }
+  }
+}
+
+template <int ET, int KMAX, bool FL>
+static void launch_route(dim3 grid, size_t shm, hipStream_t st, const bf16_t* x, const bf16_t* gate,
+                         const bf16_t* li, const float* bias, int64_t N, int D, int E, int k,
+                         int gating, int need_ssum, bf16_t* lo, int64_t* ti, float* tw, float* lse,
+                         int32_t* rl, RouteWs ws) {
+  hipLaunchKernelGGL((route_fwd_kernel<ET, KMAX, FL>), grid, dim3(kRouteThreads), shm, st, x, gate,
+                     li, bias, N, D, E, k, gating, need_ssum, lo, ti, tw, lse, rl, ws);
+}
+
+template <int ET, int KMAX>
+static void launch_route_fl(bool fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
+                            const bf16_t* gate, const bf16_t* li, const float* bias, int64_t N,
+                            int D, int E, int k, int gating, int need_ssum, bf16_t* lo, int64_t* ti,
+                            float* tw, float* lse, int32_t* rl, RouteWs ws) {
+  if (fl)
+    launch_route<ET, KMAX, true>(grid, shm, st, x, gate, li, bias, N, D, E, k, gating, need_ssum,
+                                 lo, ti, tw, lse, rl, ws);
+  else
+    launch_route<ET, KMAX, false>(grid, shm, st, x, gate, li, bias, N, D, E, k, gating, need_ssum,
+                                  lo, ti, tw, lse, rl, ws);
+}
+
+template <int ET>
+static void launch_route_k(int k, bool fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
+                           const bf16_t* gate, const bf16_t* li, const float* bias, int64_t N,
+                           int D, int E, int gating, int need_ssum, bf16_t* lo, int64_t* ti,
+                           float* tw, float* lse, int32_t* rl, RouteWs ws) {
+#define FFMOE_RK(KM)                                                                           \
+  launch_route_fl<ET, KM>(fl, grid, shm, st, x, gate, li, bias, N, D, E, k, gating, need_ssum, \
+                          lo, ti, tw, lse, rl, ws)
+  if (k <= 2)
+    FFMOE_RK(2);
+  else if (k <= 4)
+    FFMOE_RK(4);
+  else if (k <= 8)
+    FFMOE_RK(8);
+  else
+    FFMOE_RK(16);
+#undef FFMOE_RK
+}
+
+}  // namespace ffmoe
+
+using namespace ffmoe;
+
+// Workspace: hist, psum, ssum [nb][E], zpart [nb], then (256-byte aligned)
+// rank_local [N*k] int32.
+static size_t rank_local_offset(int64_t N, int E) {
+  const int64_t nb = route_blocks(N);
+  return (static_cast<size_t>(nb * E * 3 + nb) * 4 + 255) / 256 * 256;
+}
+
+extern "C" size_t ffmoe_route_workspace_bytes(int64_t N, int E, int k) {
+  return rank_local_offset(N, E) + static_cast<size_t>(N) * k * 4;
+}
+
+extern "C" int ffmoe_route_fwd(const void* x, const void* gate, const void* logits_in,
+                               const float* expert_bias, int64_t N, int D, int E, int k,
+                               int gating, int need_sigmoid_sum, void* logits_out,
+                               int64_t* topk_idx, float* topk_w, float* lse, void* workspace,
+                               void* stream) {
+  if (N <= 0) return set_error("ffmoe_route_fwd: N must be positive");
+  if (E < 1 || E > FFMOE_MAX_EXPERTS) return set_error("ffmoe_route_fwd: E out of range [1, 256]");
+  if (k < 1 || k > E || k > FFMOE_MAX_TOPK)
+    return set_error("ffmoe_route_fwd: top_k must be in [1, min(E, 16)]");
+  if (logits_in == nullptr && (D <= 0 || D % 8 != 0))
+    return set_error("ffmoe_route_fwd: D must be a positive multiple of 8");
+  if (gating != FFMOE_GATING_SOFTMAX && gating != FFMOE_GATING_SIGMOID)
+    return set_error("ffmoe_route_fwd: unknown gating");
+  if (workspace == nullptr || topk_idx == nullptr || topk_w == nullptr)
+    return set_error("ffmoe_route_fwd: null output");
+  const int ET = E <= 16 ? 1 : E <= 32 ? 2 : E <= 64 ? 4 : E <= 128 ? 8 : 16;
+  const int LS = ET * 16 + 2;  // bf16 elements per LDS logits row
+  const size_t shm = static_cast<size_t>(kRouteTokens) * LS * 2 +
+                     (2 * static_cast<size_t>(kRouteTokens) * k + kRouteTokens) * 4;
+  RouteWs ws = route_ws(workspace, N, E);
+  int32_t* rl = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + rank_local_offset(N, E));
+  const dim3 grid(static_cast<unsigned>(route_blocks(N)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool fl = logits_in != nullptr;
+  auto xb = static_cast<const bf16_t*>(x);
+  auto gb = static_cast<const bf16_t*>(gate);
+  auto lb = static_cast<const bf16_t*>(logits_in);
+  auto lo = static_cast<bf16_t*>(logits_out);
+#define FFMOE_RE(ETV)                                                                           \
+  launch_route_k<ETV>(k, fl, grid, shm, st, xb, gb, lb, expert_bias, N, D, E, gating,           \
+                      need_sigmoid_sum, lo, topk_idx, topk_w, lse, rl, ws)
+  switch (ET) {
+    case 1: FFMOE_RE(1); break;
+    case 2: FFMOE_RE(2); break;
+    case 4: FFMOE_RE(4); break;
+    case 8: FFMOE_RE(8); break;
+    default: FFMOE_RE(16); break;
+  }
+#undef FFMOE_RE
+  if (check_launch("route_fwd_kernel")) return 1;
+  return clear_error();
+}
+
+extern "C" int ffmoe_route_scan(int64_t N, int E, int k, int mt, int gemm_bm, float aux_coeff,
+                                float z_coeff, int gating, void* workspace, int32_t* counts,
+                                int32_t* offsets, int32_t* tile_offsets, float* stats,
+                                int32_t* istats, void* stream) {
+  if (N <= 0 || E < 1 || E > FFMOE_MAX_EXPERTS) return set_error("ffmoe_route_scan: bad N/E");
+  if (mt < 0 || gemm_bm <= 0) return set_error("ffmoe_route_scan: bad mt/gemm_bm");
+  RouteWs ws = route_ws(workspace, N, E);
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), N,
+                     route_blocks(N), E, k, mt, gemm_bm, aux_coeff, z_coeff, gating, ws, counts,
+                     offsets, tile_offsets, stats, istats);
+  if (check_launch("route_scan_kernel")) return 1;
+  return clear_error();
+}
+
+extern "C" int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
+                             const int32_t* offsets, const int32_t* counts, int64_t N, int D, int E,
+                             int k, int mt, int capacity_mode, void* workspace, void* x_sorted,
+                             int32_t* row_of, void* stream) {
+  if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_permute: D must be a positive multiple of 8");
+  if (k < 1 || k > FFMOE_MAX_TOPK || E < 1 || E > FFMOE_MAX_EXPERTS)
+    return set_error("ffmoe_permute: bad k/E");
+  RouteWs ws = route_ws(workspace, N, E);
+  const int32_t* rl =
+      reinterpret_cast<const int32_t*>(static_cast<char*>(workspace) + rank_local_offset(N, E));
+  const dim3 grid(static_cast<unsigned>((N + kPermTokens - 1) / kPermTokens));
+  hipLaunchKernelGGL(permute_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const bf16_t*>(x), topk_idx, topk_w, offsets, counts, rl, ws.hist,
+                     N, D, E, k, mt, capacity_mode, static_cast<bf16_t*>(x_sorted), row_of);
+  if (check_launch("permute_kernel")) return 1;
+  return clear_error();
+}

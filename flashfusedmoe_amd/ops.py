@@ -1,0 +1,200 @@
+"""torch custom ops over libffmoe.so: routing, expert forward, expert backward.
+
+Each op enqueues HIP kernels on the current stream through the C ABI of
+include/ffmoe.h and allocates its outputs with the torch caching allocator.
+Fake (meta) implementations make the ops traceable by torch.compile.
+
+Only bfloat16 CUDA(ROCm) tensors are accepted; there is no other path.
+"""
+
+from typing import List, Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib as L
+
+_BF16 = torch.bfloat16
+
+
+def _require(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_bf16_gpu(name, t):
+    if t.device.type != "cuda":
+        raise RuntimeError(f"ffmoe: {name} must be on a ROCm GPU (got {t.device}); "
+                           "the fused MoE kernels have no CPU path")
+    if t.dtype != _BF16:
+        raise TypeError(f"ffmoe: {name} must be bfloat16 (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"ffmoe: {name} must be contiguous")
+
+
+# ---------------------------------------------------------------------------
+# routing: gate GEMM + top-k + histogram scan + losses/metrics
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("ffmoe::route", mutates_args=())
+def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, gating: int,
+          mt: int, aux_coeff: float, z_coeff: float, need_ssum: bool) -> List[Tensor]:
+    """Returns [logits bf16 [N,E], topk_idx int64 [N,k], topk_w fp32 [N,k],
+    lse fp32 [N], counts int32 [E], offsets int32 [E+1], tile_offsets int32
+    [E+1], stats fp32 [4], istats int32 [4], workspace uint8]."""
+    _check_bf16_gpu("hidden_states", x)
+    _check_bf16_gpu("gate_weight", gate)
+    N, D = x.shape
+    E = gate.shape[0]
+    k = top_k
+    dev = x.device
+    ws = torch.empty(L.route_workspace_bytes(N, E, k), dtype=torch.uint8, device=dev)
+    logits = torch.empty(N, E, dtype=_BF16, device=dev)
+    topk_idx = torch.empty(N, k, dtype=torch.int64, device=dev)
+    topk_w = torch.empty(N, k, dtype=torch.float32, device=dev)
+    lse = torch.empty(N, dtype=torch.float32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    tile_offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    stats = torch.empty(L.NUM_STATS, dtype=torch.float32, device=dev)
+    istats = torch.empty(L.NUM_ISTATS, dtype=torch.int32, device=dev)
+    bias = None
+    if expert_bias is not None:
+        bias = expert_bias.to(device=dev, dtype=torch.float32).contiguous()
+    st = L.stream_ptr(dev)
+    L.call("ffmoe_route_fwd", L.ptr(x), L.ptr(gate), None, L.ptr(bias), N, D, E, k, gating,
+           int(need_ssum), L.ptr(logits), L.ptr(topk_idx), L.ptr(topk_w), L.ptr(lse), L.ptr(ws), st)
+    L.call("ffmoe_route_scan", N, E, k, mt, L.gemm_tile_rows(), aux_coeff, z_coeff, gating,
+           L.ptr(ws), L.ptr(counts), L.ptr(offsets), L.ptr(tile_offsets), L.ptr(stats),
+           L.ptr(istats), st)
+    return [logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats, ws]
+
+
+@route.register_fake
+def _route_fake(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, need_ssum):
+    N, D = x.shape
+    E = gate.shape[0]
+    f = lambda *s, dtype: x.new_empty(s, dtype=dtype)  # noqa: E731
+    return [f(N, E, dtype=_BF16), f(N, top_k, dtype=torch.int64), f(N, top_k, dtype=torch.float32),
+            f(N, dtype=torch.float32), f(E, dtype=torch.int32), f(E + 1, dtype=torch.int32),
+            f(E + 1, dtype=torch.int32), f(L.NUM_STATS, dtype=torch.float32),
+            f(L.NUM_ISTATS, dtype=torch.int32), f(0, dtype=torch.uint8)]
+
+
+# ---------------------------------------------------------------------------
+# experts forward: permute + up GEMM/GLU + down GEMM + combine
+# ---------------------------------------------------------------------------
+
+def _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, save_up, st):
+    T, D = xs.shape
+    E, H2, _ = w_up.shape
+    H = H2 // 2
+    dev = xs.device
+    up = torch.empty(T, H2, dtype=_BF16, device=dev) if save_up else None
+    act = torch.empty(T, H, dtype=_BF16, device=dev)
+    down = torch.empty(T, D, dtype=_BF16, device=dev)
+    L.call("ffmoe_gemm_up_glu", L.ptr(xs), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), E, T,
+           D, H, activation, L.ptr(up), L.ptr(act), st)
+    L.call("ffmoe_gemm_down", L.ptr(act), L.ptr(w_down), L.ptr(offsets), L.ptr(tile_offsets), E, T,
+           H, D, L.ptr(down), st)
+    return up, act, down
+
+
+@torch.library.custom_op("ffmoe::experts_forward", mutates_args=())
+def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, topk_w: Tensor,
+                    counts: Tensor, offsets: Tensor, tile_offsets: Tensor, ws: Tensor, top_k: int,
+                    activation: int, mt: int, capacity_mode: bool,
+                    save_activations: bool) -> List[Tensor]:
+    """Returns [out bf16 [N,D], topk_w fp32 [N,k] (renormalised under capacity
+    dropping), row_of int32 [N*k], x_sorted bf16 [N*k,D], up, act, down] where
+    up/act/down are empty when save_activations is False."""
+    _check_bf16_gpu("w_up", w_up)
+    _check_bf16_gpu("w_down", w_down)
+    N, D = x.shape
+    E = w_up.shape[0]
+    k = top_k
+    T = N * k
+    dev = x.device
+    st = L.stream_ptr(dev)
+    tw = topk_w.clone()
+    xs = torch.empty(T, D, dtype=_BF16, device=dev)
+    row_of = torch.empty(T, dtype=torch.int32, device=dev)
+    L.call("ffmoe_permute", L.ptr(x), L.ptr(topk_idx), L.ptr(tw), L.ptr(offsets), L.ptr(counts),
+           N, D, E, k, mt, int(capacity_mode), L.ptr(ws), L.ptr(xs), L.ptr(row_of), st)
+    up, act, down = _up_down(xs, w_up, w_down, offsets, tile_offsets, activation,
+                             save_activations, st)
+    out = torch.empty(N, D, dtype=_BF16, device=dev)
+    L.call("ffmoe_combine", L.ptr(down), L.ptr(row_of), L.ptr(tw), None, N, D, k, L.ptr(out), st)
+    empty = x.new_empty(0)
+    if not save_activations:
+        return [out, tw, row_of, xs, empty, empty.clone(), empty.clone()]
+    return [out, tw, row_of, xs, up, act, down]
+
+
+@experts_forward.register_fake
+def _experts_forward_fake(x, w_up, w_down, topk_idx, topk_w, counts, offsets, tile_offsets, ws,
+                          top_k, activation, mt, capacity_mode, save_activations):
+    N, D = x.shape
+    H2 = w_up.shape[1]
+    T = N * top_k
+    e = x.new_empty
+    if save_activations:
+        acts = [e(T, H2), e(T, H2 // 2), e(T, D)]
+    else:
+        acts = [e(0), e(0), e(0)]
+    return [e(N, D), topk_w.new_empty(topk_w.shape), e(T, dtype=torch.int32), e(T, D), *acts]
+
+
+# ---------------------------------------------------------------------------
+# experts backward
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("ffmoe::experts_backward", mutates_args=())
+def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: Tensor,
+                     logits: Tensor, topk_idx: Tensor, topk_w: Tensor, lse: Tensor, counts: Tensor,
+                     offsets: Tensor, tile_offsets: Tensor, row_of: Tensor, xs: Tensor, up: Tensor,
+                     act: Tensor, down: Tensor, g_aux: Optional[Tensor], g_z: Optional[Tensor],
+                     top_k: int, activation: int, gating: int, capacity_mode: bool,
+                     aux_coeff: float, z_coeff: float) -> List[Tensor]:
+    """Returns [grad_hidden [N,D], grad_gate [E,D], grad_w_up [E,2H,D],
+    grad_w_down [E,D,H]], all bf16.  Empty up/act/down trigger recompute."""
+    _check_bf16_gpu("grad_output", go)
+    N, D = x.shape
+    E, H2, _ = w_up.shape
+    H = H2 // 2
+    k = top_k
+    T = N * k
+    dev = x.device
+    st = L.stream_ptr(dev)
+    if up.numel() == 0:  # recompute_activations: same kernels, same bits
+        up, act, down = _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, True, st)
+    wgo = torch.empty(T, D, dtype=_BF16, device=dev)
+    gl = torch.empty(N, E, dtype=_BF16, device=dev)
+    ga = None if g_aux is None else g_aux.to(device=dev, dtype=torch.float32).contiguous()
+    gz = None if g_z is None else g_z.to(device=dev, dtype=torch.float32).contiguous()
+    L.call("ffmoe_route_bwd", L.ptr(go), L.ptr(down), L.ptr(row_of), L.ptr(topk_idx),
+           L.ptr(topk_w), L.ptr(logits), L.ptr(lse), L.ptr(counts), L.ptr(ga), L.ptr(gz),
+           aux_coeff, z_coeff, N, D, E, k, gating, int(capacity_mode), L.ptr(wgo), L.ptr(gl),
+           None, st)
+    gup = torch.empty(T, H2, dtype=_BF16, device=dev)
+    L.call("ffmoe_gemm_dgrad_glu", L.ptr(wgo), L.ptr(w_down), L.ptr(up), L.ptr(offsets),
+           L.ptr(tile_offsets), E, T, D, H, activation, L.ptr(gup), st)
+    ghb = torch.empty(T, D, dtype=_BF16, device=dev)
+    L.call("ffmoe_gemm_dgrad", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), E, T,
+           H, D, L.ptr(ghb), st)
+    # the two small dense gate products are plain library GEMMs (hipBLASLt)
+    addend = torch.matmul(gl, gate)
+    dx = torch.empty(N, D, dtype=_BF16, device=dev)
+    L.call("ffmoe_combine", L.ptr(ghb), L.ptr(row_of), None, L.ptr(addend), N, D, k, L.ptr(dx), st)
+    dwd = torch.empty(E, D, H, dtype=_BF16, device=dev)
+    L.call("ffmoe_gemm_wgrad", L.ptr(wgo), L.ptr(act), L.ptr(offsets), E, D, H, L.ptr(dwd), st)
+    dwu = torch.empty(E, H2, D, dtype=_BF16, device=dev)
+    L.call("ffmoe_gemm_wgrad", L.ptr(gup), L.ptr(xs), L.ptr(offsets), E, H2, D, L.ptr(dwu), st)
+    dgate = torch.matmul(gl.t().contiguous(), x)
+    return [dx, dgate, dwu, dwd]
+
+
+@experts_backward.register_fake
+def _experts_backward_fake(go, x, gate, w_up, w_down, *rest):
+    return [x.new_empty(x.shape), gate.new_empty(gate.shape), w_up.new_empty(w_up.shape),
+            w_down.new_empty(w_down.shape)]

@@ -1,0 +1,240 @@
+/*
+ * ffmoe.h -- C ABI of libffmoe.so, the MI355X (gfx950) kernels of the fused
+ * Mixture-of-Experts layer (non-expert-parallel path).
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are DEVICE pointers owned by the caller (the torch
+ *     caching allocator); the library never allocates device memory.
+ *   - Tensors are dense and row-major.  "bf16" is IEEE bfloat16 stored as
+ *     uint16_t; int64 index tensors match torch.int64.
+ *   - `stream` is a hipStream_t passed as void*; every kernel is enqueued on it
+ *     and nothing synchronises the host.
+ *   - Return value: 0 on success.  Nonzero means the arguments were rejected
+ *     (nothing was launched) or a launch failed; ffmoe_last_error() returns a
+ *     message describing the most recent failure on the calling thread.
+ *
+ * Token/row vocabulary (identical to the reference's)
+ *   N tokens, D model dim, E experts, k = top_k, H = ffn_dim / 2.
+ *   Entry j = n*k + s is token n's s-th choice (slot).  Each expert's entries
+ *   are ranked in ascending j (the reference's stable argsort,
+ *   fused_moe.py:344-348).  Entries of expert e with rank < mt own a row of the
+ *   expert-sorted activation matrix; this library stores those rows COMPACTLY:
+ *   row = offsets[e] + rank, offsets[e] = sum_{e'<e} min(count[e'], mt).  The
+ *   reference's padded coordinate is e*mt + rank (moe_ops.py:84-98); both name
+ *   the same permutation.  row_of[j] holds the row, or
+ *     FFMOE_ROW_DROPPED (-1): entry dropped, contributes zero (capacity
+ *                              sentinel row, fused_moe.py:428-430), or
+ *     FFMOE_ROW_ALIAS0  (-2): entry overflowed mt and reads row 0 like the
+ *                              reference's e2b = 0 (moe_ops.py:87-91, :138-140).
+ */
+#ifndef FFMOE_H
+#define FFMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FFMOE_ROW_DROPPED (-1)
+#define FFMOE_ROW_ALIAS0 (-2)
+
+/* gating */
+#define FFMOE_GATING_SOFTMAX 0
+#define FFMOE_GATING_SIGMOID 1
+/* activation */
+#define FFMOE_ACT_SWIGLU 0
+#define FFMOE_ACT_GEGLU 1
+#define FFMOE_ACT_RELU2 2
+
+/* limits enforced by the entry points */
+#define FFMOE_MAX_EXPERTS 256
+#define FFMOE_MAX_TOPK 16
+
+/* layout of the `stats` output of ffmoe_route_scan (fp32 slots) */
+#define FFMOE_STAT_AUX 0          /* aux_loss (coefficient applied)            */
+#define FFMOE_STAT_Z 1            /* z_loss (coefficient applied)              */
+#define FFMOE_STAT_IMBALANCE 2    /* max count / (mean count + 1e-6)           */
+#define FFMOE_STAT_DROP_FRAC 3    /* dropped entries / (N*k)                   */
+#define FFMOE_NUM_STATS 4
+/* layout of the `istats` output of ffmoe_route_scan (int32 slots) */
+#define FFMOE_ISTAT_MAX 0         /* max tokens_per_expert                     */
+#define FFMOE_ISTAT_MIN 1         /* min tokens_per_expert                     */
+#define FFMOE_ISTAT_DROPPED 2     /* entries without a row (rank >= mt)        */
+#define FFMOE_NUM_ISTATS 4
+
+/* Message for the most recent failure on this thread ("" if none). */
+const char* ffmoe_last_error(void);
+
+/* Library version, for the loader's sanity check. */
+int ffmoe_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Routing forward                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of workspace ffmoe_route_fwd / ffmoe_route_scan / ffmoe_permute share
+ * for a problem of N tokens, E experts and top_k = k.  The same workspace
+ * (and the same N, E, k) must be passed to all three calls of one forward. */
+size_t ffmoe_route_workspace_bytes(int64_t N, int E, int k);
+
+/* Gate GEMM + scoring + top-k + per-block routing statistics.
+ * Replaces: the gate GEMM `hidden @ gate.T` (fused_moe.py:334, :1165),
+ *   `fused_topk_routing` and its kernels (fused_topk.py:30-179, via
+ *   `_apply_routing` fast path fused_moe.py:139-142), the `bincount` and
+ *   per-expert sums of the losses block (fused_moe.py:1176-1194).
+ * x [N,D] bf16, gate [E,D] bf16.  If logits_in != NULL the gate GEMM is
+ * skipped and those bf16 logits [N,E] are routed instead (the reference's
+ * `fused_topk_routing(logits, ...)` boundary); otherwise the bf16 logits are
+ * written to logits_out [N,E] (may be NULL).
+ * expert_bias [E] fp32 or NULL: added to the scores for SELECTION only
+ *   (fused_moe.py:163-179, :183-193); weights use unbiased scores.
+ * Outputs: topk_idx [N,k] int64, topk_w [N,k] fp32 (slots in descending
+ *   selection order; lowest expert index wins a tie, fused_topk.py:63-70),
+ *   lse [N] fp32 (logsumexp of the fp32 logits; may be NULL).
+ * Selection rule, weights: softmax over the selected logits, or sigmoid
+ *   scores / (sum + 1e-6) (fused_topk.py:72-78, :128-132).
+ * need_sigmoid_sum: also accumulate sum_n sigmoid(logit) per expert (the
+ *   sigmoid aux loss, fused_moe.py:1187-1188). */
+int ffmoe_route_fwd(const void* x, const void* gate, const void* logits_in,
+                    const float* expert_bias, int64_t N, int D, int E, int k,
+                    int gating, int need_sigmoid_sum, void* logits_out,
+                    int64_t* topk_idx, float* topk_w, float* lse,
+                    void* workspace, void* stream);
+
+/* Global prefix over the per-block expert histograms, losses and metrics.
+ * Replaces: `bincount`/`cumsum` (fused_moe.py:346-348), the overflow check's
+ *   max (fused_moe.py:401), the aux/z-loss and metrics reductions
+ *   (fused_moe.py:1176-1217).
+ * mt: rows per expert (max_tokens, or the capacity when capacity dropping).
+ * gemm_bm: row-tile height of the grouped GEMMs; tile_offsets[e] is the
+ *   number of gemm_bm-row tiles of experts < e.
+ * Outputs: counts [E] int32 (tokens_per_expert), offsets [E+1] int32,
+ *   tile_offsets [E+1] int32, stats [FFMOE_NUM_STATS] fp32,
+ *   istats [FFMOE_NUM_ISTATS] int32. */
+int ffmoe_route_scan(int64_t N, int E, int k, int mt, int gemm_bm,
+                     float aux_coeff, float z_coeff, int gating,
+                     void* workspace, int32_t* counts, int32_t* offsets,
+                     int32_t* tile_offsets, float* stats, int32_t* istats,
+                     void* stream);
+
+/* Stable permutation of tokens into expert-sorted compact rows.
+ * Replaces: `fused_routing_scatter` (moe_ops.py:43-149) and the capacity
+ *   keep-mask / renormalisation (fused_moe.py:350-390, :428-430).
+ * x [N,D] bf16 -> x_sorted [rows, D] bf16 (rows = offsets[E]), row_of [N*k].
+ * capacity_mode: 1 = entries with rank >= mt are dropped (FFMOE_ROW_DROPPED)
+ *   and topk_w is renormalised in place; 0 = overflow entries alias row 0
+ *   (FFMOE_ROW_ALIAS0) when expert 0 has a row, else FFMOE_ROW_DROPPED. */
+int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
+                  const int32_t* offsets, const int32_t* counts, int64_t N, int D,
+                  int E, int k, int mt, int capacity_mode, void* workspace,
+                  void* x_sorted, int32_t* row_of, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Expert grouped GEMMs (bf16 MFMA, fp32 accumulate, bf16 out).             */
+/* Row groups come from offsets[E+1] and tile_offsets[E+1] on the device;   */
+/* max_rows is the host-side upper bound of offsets[E] (N*k).               */
+/* ------------------------------------------------------------------------ */
+
+/* up = x_sorted · w_up[e]^T and the fused GLU:
+ *   up_out [rows, 2H] (pre-activation, may be NULL), act_out [rows, H].
+ * Replaces: up bmm (fused_moe.py:435) + `activation_forward`
+ *   (activations.py:27-74, :145-186).  w_up [E, 2H, D]: rows [0,H) gate half,
+ *   [H,2H) up half. */
+int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up,
+                      const int32_t* offsets, const int32_t* tile_offsets, int E,
+                      int64_t max_rows, int D, int H, int activation,
+                      void* up_out, void* act_out, void* stream);
+
+/* down [rows, D] = act · w_down[e]^T.  w_down [E, D, H].
+ * Replaces: down bmm (fused_moe.py:441). */
+int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
+                    const int32_t* tile_offsets, int E, int64_t max_rows, int H,
+                    int D, void* down_out, void* stream);
+
+/* gup [rows, 2H] = GLU_backward(wgo · w_down[e], up).
+ * Replaces: dX-down bmm (fused_moe.py:547) + `activation_backward`
+ *   (activations.py:77-142, :189-231). */
+int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,
+                         const int32_t* offsets, const int32_t* tile_offsets,
+                         int E, int64_t max_rows, int D, int H, int activation,
+                         void* gup_out, void* stream);
+
+/* ghb [rows, D] = gup · w_up[e].  Replaces: dX-up bmm (fused_moe.py:553). */
+int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t* offsets,
+                     const int32_t* tile_offsets, int E, int64_t max_rows, int H,
+                     int D, void* ghb_out, void* stream);
+
+/* Row-tile height (BM) of the grouped GEMMs: pass it as `gemm_bm` to
+ * ffmoe_route_scan so tile_offsets match the GEMM kernels.  No reference
+ * counterpart (the reference pads every expert to max_tokens rows). */
+int ffmoe_gemm_tile_rows(void);
+
+/* Selects how MN-contiguous GEMM operands are read from LDS: 1 (default) =
+ * ds_read_b64_tr_b16 transpose reads, 0 = element-wise reads.  Returns the
+ * previous setting.  Both give identical results; the switch exists so the
+ * transpose-read path can be verified against the element-wise one.  No
+ * reference counterpart. */
+int ffmoe_set_lds_transpose(int enable);
+
+/* c[e] [M, Nc] = a[rows_e]^T · b[rows_e]; a [rows, M], b [rows, Nc].
+ * Experts with no rows get zeros.
+ * Replaces: dW-down and dW-up bmm (fused_moe.py:564-565). */
+int ffmoe_gemm_wgrad(const void* a, const void* b, const int32_t* offsets, int E,
+                     int M, int Nc, void* c_out, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Combine / routing backward / dX reduce                                   */
+/* ------------------------------------------------------------------------ */
+
+/* out[n] = sum_s w[n,s] * rows[row_of[n*k+s]] accumulated in fp32 in slot
+ * order; w is bf16(topk_w) (fused_moe.py:412) or, if topk_w is NULL, 1.
+ * addend [N,D] bf16 or NULL: out = bf16(bf16(sum) + addend) (the reference's
+ * `grad_hidden + gl @ gate`, fused_moe.py:590).
+ * Replaces: `fused_gather_reduce` (moe_ops.py:156-241). */
+int ffmoe_combine(const void* rows, const int32_t* row_of, const float* topk_w,
+                  const void* addend, int64_t N, int D, int k, void* out,
+                  void* stream);
+
+/* Routing backward, one pass per token.
+ * Replaces: routing-weight grad (fused_moe.py:527-535), `fused_weighted_scatter`
+ *   (moe_ops.py:248-332), softmax/sigmoid top-k backward + scatter_add
+ *   (fused_moe.py:567-589), and the z-loss / sigmoid aux-loss gradients that
+ *   autograd produces through the losses block (fused_moe.py:1178-1194).
+ * go [N,D] bf16, down [rows,D] bf16, row_of [N*k], topk_idx, topk_w fp32,
+ * logits [N,E] bf16, lse [N] fp32, counts [E] int32.
+ * g_aux, g_z: fp32 device scalars (upstream grads of the losses) or NULL.
+ * capacity_mode: 1 -> grads of tokens whose kept weights sum to 0 are zeroed
+ *   (fused_moe.py:569-571).
+ * Outputs: wgo [rows, D] bf16 (go[n] * bf16(w) at each owned row),
+ *   grad_logits [N,E] bf16, grad_w [N,k] fp32 (may be NULL). */
+int ffmoe_route_bwd(const void* go, const void* down, const int32_t* row_of,
+                    const int64_t* topk_idx, const float* topk_w,
+                    const void* logits, const float* lse, const int32_t* counts,
+                    const float* g_aux, const float* g_z, float aux_coeff,
+                    float z_coeff, int64_t N, int D, int E, int k, int gating,
+                    int capacity_mode, void* wgo, void* grad_logits,
+                    float* grad_w, void* stream);
+
+/* Standalone GLU kernels (the reference's `activation_forward` /
+ * `activation_backward`, activations.py:145-231).  up [M, 2H] bf16 ->
+ * act [M, H]; grad_act [M, H], up [M, 2H] -> grad_up [M, 2H]. */
+int ffmoe_glu_fwd(const void* up, int64_t M, int H, int activation, void* act,
+                  void* stream);
+int ffmoe_glu_bwd(const void* grad_act, const void* up, int64_t M, int H,
+                  int activation, void* grad_up, void* stream);
+
+/* Padded-layout scatter for the reference's `fused_routing_scatter` and
+ * `fused_weighted_scatter` boundaries: dst[dst_row[j]] = src[j / k] * w[j]
+ * (w = bf16(topk_w) or 1 when NULL) for every j with dst_row[j] >= 0.
+ * dst [dst_rows, D] bf16 must be pre-zeroed by the caller. */
+int ffmoe_scatter_rows(const void* src, const int64_t* dst_row, const float* w,
+                       int64_t n_entries, int k, int D, int64_t dst_rows,
+                       void* dst, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FFMOE_H */

@@ -1,0 +1,75 @@
+"""Helpers shared by the GPU parity tests."""
+
+import ctypes
+import os
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PROBE_LIB = os.path.join(ROOT, "tests", "hip", "libtrprobe.so")
+
+# bf16 tolerance of the HIP path against the CPU oracle with the reference's
+# rounding points: rtol 2e-2 / atol 2e-3 (fp32 accumulation).  Elementwise,
+# at most 0.1% of the elements may exceed atol + rtol*|expected| (a bf16
+# rounding flip upstream of a cancellation), and the relative L2 error must
+# stay below rtol.
+RTOL = 2e-2
+ATOL = 2e-3
+
+
+def check_close(actual, expected, name, rtol=RTOL, atol=ATOL, max_bad_frac=1e-3):
+    a = actual.detach().double().cpu()
+    e = expected.detach().double().cpu()
+    assert a.shape == e.shape, f"{name}: shape {a.shape} != {e.shape}"
+    assert torch.isfinite(a).all(), f"{name}: non-finite values"
+    err = (a - e).abs()
+    rel_l2 = (err.norm() / (e.norm() + 1e-30)).item()
+    bad = (err > atol + rtol * e.abs()).double().mean().item()
+    scale = e.abs().max().item()
+    assert rel_l2 < rtol, f"{name}: relative L2 error {rel_l2:.3e} >= {rtol}"
+    assert bad <= max_bad_frac, f"{name}: {bad:.2e} of elements outside atol+rtol*|e|"
+    assert err.max().item() <= 10 * (atol + rtol * scale), \
+        f"{name}: max abs error {err.max().item():.3e} (scale {scale:.3e})"
+    return rel_l2
+
+
+def seeded(N, D, ffn, E, seed=0, gate_scale=None, w_scale=None, dtype=torch.bfloat16):
+    """Inputs generated on the CPU in fp32 then cast: CPU oracle and GPU see
+    identical bits.  Default weights ~ N(0, 1/fan_in)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(N, D, generator=g)
+    gs = gate_scale if gate_scale is not None else D ** -0.5
+    gate = torch.randn(E, D, generator=g) * gs
+    wu = torch.randn(E, ffn, D, generator=g) * (w_scale if w_scale is not None else D ** -0.5)
+    wd = torch.randn(E, D, ffn // 2, generator=g) * (w_scale if w_scale is not None else (ffn // 2) ** -0.5)
+    return tuple(t.to(dtype) for t in (x, gate, wu, wd))
+
+
+def cuda(*ts):
+    return tuple(t.cuda() for t in ts)
+
+
+def probe_lds_transpose():
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.ffmoe_probe_lds_tr.argtypes = [ctypes.c_void_p]
+    lib.ffmoe_probe_lds_tr.restype = ctypes.c_int
+    out = torch.zeros(64 * 4, dtype=torch.int16, device="cuda")
+    assert lib.ffmoe_probe_lds_tr(out.data_ptr()) == 0
+    return out.cpu().numpy().astype(np.uint16).reshape(64, 4)
+
+
+def expected_rows(idx, E, mt, capacity_mode):
+    """Compact row of every entry from the oracle's stable permutation."""
+    from oracle import routing as R
+    idx = np.asarray(idx)
+    _, counts, _, rank = R.stable_permutation(idx, E)
+    rows = np.minimum(counts, mt)
+    off = np.zeros(E + 1, dtype=np.int64)
+    off[1:] = np.cumsum(rows)
+    flat = idx.reshape(-1)
+    own = rank < mt
+    out = np.where(own, off[flat] + rank, -1)
+    if not capacity_mode and counts[0] > 0:
+        out = np.where(own, out, -2)
+    return out, counts, off

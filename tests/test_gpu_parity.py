@@ -1,0 +1,381 @@
+"""GPU parity: the HIP path (libffmoe.so) against the CPU oracle on identical
+seeded inputs.  Integer/index results (top-k indices, counts, the token
+permutation) must be bit-exact; floating-point results must match within the
+bf16 tolerance of gpu_helpers.check_close (rtol 2e-2, atol 2e-3, fp32
+accumulation)."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import check_close, cuda, expected_rows, probe_lds_transpose, seeded
+from oracle import fused as F_
+from oracle import routing as R
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib():
+    from flashfusedmoe_amd import _lib as L
+    L.load()
+    yield L
+    L.set_lds_transpose(True)
+
+
+# --- the gfx950 LDS transpose read the MN-contiguous GEMM operands rely on -----
+
+def test_lds_transpose_read_lane_layout():
+    got = probe_lds_transpose()
+    for lane in range(64):
+        g, i = lane // 16, lane % 16
+        col = (g & 1) * 16 + i
+        rows = [(g >> 1) * 8 + q for q in range(4)]
+        assert list(got[lane]) == [r * 64 + col for r in rows], f"lane {lane}: {list(got[lane])}"
+
+
+# --- routing -------------------------------------------------------------------
+
+def _tie_heavy_logits(N, E, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(-3, 4, (N, E), generator=g).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (4, 1), (16, 4), (7, 3), (64, 8), (256, 8), (256, 16), (33, 5)])
+@pytest.mark.parametrize("gating", ["softmax", "sigmoid"])
+@pytest.mark.parametrize("ties", [False, True])
+def test_topk_routing_bit_exact(E, k, gating, ties):
+    from flashfusedmoe_amd.kernels import fused_topk_routing
+    N = 1000
+    if ties:
+        logits = _tie_heavy_logits(N, E, E * 7 + k)
+    else:
+        g = torch.Generator().manual_seed(E + k)
+        logits = torch.randn(N, E, generator=g).to(torch.bfloat16)
+    w, idx = fused_topk_routing(logits.cuda(), gating, k)
+    rw, ridx = R.route(logits.float().numpy(), k, gating)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("N,D,E", [(8192, 1024, 8), (777, 256, 64), (4096, 7168, 256), (5, 64, 16)])
+def test_gate_logits_and_routing(N, D, E):
+    """The fused MFMA gate GEMM rounds fp32 sums to bf16: at most one bf16 ulp
+    from the correctly rounded product (summation order differs), and routing
+    of the produced logits is bit-exact."""
+    from flashfusedmoe_amd import ops
+    x, gate, _, _ = seeded(N, D, 16, E, seed=N + E)
+    k = min(8, E)
+    outs = ops.route(x.cuda(), gate.cuda(), None, k, 0, R.estimate_max_tokens(N, k, E), 0.0, 0.0,
+                     False)
+    logits, idx, w = outs[0].cpu(), outs[1].cpu(), outs[2].cpu()
+    exact = (x.double() @ gate.double().t()).to(torch.bfloat16)
+    diff = (logits.view(torch.int16).int() - exact.view(torch.int16).int()).abs()
+    assert diff.max().item() <= 1, "gate logits more than one bf16 ulp from the exact product"
+    assert (diff > 0).double().mean().item() < 0.02
+    rw, ridx = R.route(logits.float().numpy(), k, "softmax")
+    assert np.array_equal(idx.numpy(), ridx)
+    np.testing.assert_allclose(w.numpy(), rw, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("N,E,k,mt,cap", [(8192, 8, 2, None, False), (1000, 64, 8, 40, False),
+                                           (1000, 64, 8, 40, True), (3, 8, 2, None, False),
+                                           (4096, 256, 8, None, False)])
+def test_permutation_bit_exact(N, E, k, mt, cap):
+    from flashfusedmoe_amd import ops
+    D = 128
+    x, gate, wu, wd = seeded(N, D, 64, E, seed=N * 3 + E)
+    if mt is None:
+        mt = R.estimate_max_tokens(N, k, E)
+    xg, gg, wug, wdg = cuda(x, gate, wu, wd)
+    (logits, idx, tw, lse, counts, offsets, tile_off, stats, istats, ws) = ops.route(
+        xg, gg, None, k, 0, mt, 0.0, 0.0, False)
+    out, tw2, row_of, xs, up, act, down = ops.experts_forward(
+        xg, wug, wdg, idx, tw, counts, offsets, tile_off, ws, k, 0, mt, cap, True)
+    exp_rows, exp_counts, exp_off = expected_rows(idx.cpu().numpy(), E, mt, cap)
+    assert np.array_equal(counts.cpu().numpy(), exp_counts)
+    assert np.array_equal(offsets.cpu().numpy(), exp_off)
+    assert np.array_equal(row_of.cpu().numpy(), exp_rows)
+    own = exp_rows >= 0
+    j = np.nonzero(own)[0]
+    assert torch.equal(xs.cpu()[exp_rows[own]], x[j // k])
+    bm = __import__("flashfusedmoe_amd._lib", fromlist=["x"]).gemm_tile_rows()
+    tiles = -(-np.minimum(exp_counts, mt) // bm)
+    assert np.array_equal(tile_off.cpu().numpy()[1:], np.cumsum(tiles))
+
+
+# --- expert GEMMs against a plain fp32 PyTorch reference ------------------------
+
+def _groups(E, sizes, D, H, seed):
+    g = torch.Generator().manual_seed(seed)
+    rows = int(sum(sizes))
+    xs = torch.randn(rows, D, generator=g).to(torch.bfloat16)
+    wu = (torch.randn(E, 2 * H, D, generator=g) * D ** -0.5).to(torch.bfloat16)
+    wd = (torch.randn(E, D, H, generator=g) * H ** -0.5).to(torch.bfloat16)
+    off = np.zeros(E + 1, dtype=np.int32)
+    off[1:] = np.cumsum(sizes)
+    return xs, wu, wd, off
+
+
+@pytest.mark.parametrize("sizes,D,H", [
+    ([300, 0, 128, 1, 513, 64, 0, 127], 256, 192),
+    ([2048] * 8, 1024, 2048),
+    ([5, 17, 0, 260], 96, 40),
+])
+@pytest.mark.parametrize("tr", [True, False])
+def test_grouped_gemms_against_fp32(sizes, D, H, tr, _lib):
+    L = _lib
+    E = len(sizes)
+    xs, wu, wd, off = _groups(E, sizes, D, H, seed=sum(sizes) + D)
+    bm = L.gemm_tile_rows()
+    tiles = np.zeros(E + 1, dtype=np.int32)
+    tiles[1:] = np.cumsum([-(-s // bm) for s in sizes])
+    T = xs.shape[0]
+    dev = "cuda"
+    xs_g, wu_g, wd_g = cuda(xs, wu, wd)
+    off_g = torch.from_numpy(off).to(dev)
+    til_g = torch.from_numpy(tiles).to(dev)
+    st = L.stream_ptr()
+    L.set_lds_transpose(tr)
+    up = torch.empty(T, 2 * H, dtype=torch.bfloat16, device=dev)
+    act = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    down = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+    L.call("ffmoe_gemm_up_glu", xs_g.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
+           E, T, D, H, 0, up.data_ptr(), act.data_ptr(), st)
+    L.call("ffmoe_gemm_down", act.data_ptr(), wd_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
+           E, T, H, D, down.data_ptr(), st)
+    g = torch.Generator().manual_seed(5)
+    wgo = torch.randn(T, D, generator=g).to(torch.bfloat16).cuda()
+    gup = torch.empty(T, 2 * H, dtype=torch.bfloat16, device=dev)
+    L.call("ffmoe_gemm_dgrad_glu", wgo.data_ptr(), wd_g.data_ptr(), up.data_ptr(), off_g.data_ptr(),
+           til_g.data_ptr(), E, T, D, H, 0, gup.data_ptr(), st)
+    ghb = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+    L.call("ffmoe_gemm_dgrad", gup.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
+           E, T, H, D, ghb.data_ptr(), st)
+    dwd = torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
+    L.call("ffmoe_gemm_wgrad", wgo.data_ptr(), act.data_ptr(), off_g.data_ptr(), E, D, H,
+           dwd.data_ptr(), st)
+    dwu = torch.empty(E, 2 * H, D, dtype=torch.bfloat16, device=dev)
+    L.call("ffmoe_gemm_wgrad", gup.data_ptr(), xs_g.data_ptr(), off_g.data_ptr(), E, 2 * H, D,
+           dwu.data_ptr(), st)
+    torch.cuda.synchronize()
+    L.set_lds_transpose(True)
+
+    # fp32 reference per expert on the GPU, from the kernels' own bf16 inputs
+    f = lambda t: t.float()  # noqa: E731
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b > a:
+            ref_up = f(xs_g[a:b]) @ f(wu_g[e]).t()
+            check_close(up[a:b], ref_up, f"up[e={e}]")
+            gg, uu = f(up[a:b, :H]), f(up[a:b, H:])
+            check_close(act[a:b], torch.nn.functional.silu(gg) * uu, f"act[e={e}]")
+            check_close(down[a:b], f(act[a:b]) @ f(wd_g[e]).t(), f"down[e={e}]")
+            gact = (f(wgo[a:b]) @ f(wd_g[e])).to(torch.bfloat16).float()
+            s = torch.sigmoid(gg)
+            ref_gu = gact * gg * s
+            ref_gg = gact * uu * (s * (1 + gg * (1 - s)))
+            check_close(gup[a:b], torch.cat([ref_gg, ref_gu], 1), f"gup[e={e}]")
+            check_close(ghb[a:b], f(gup[a:b]) @ f(wu_g[e]), f"ghb[e={e}]")
+            check_close(dwd[e], f(wgo[a:b]).t() @ f(act[a:b]), f"dW_down[e={e}]")
+            check_close(dwu[e], f(gup[a:b]).t() @ f(xs_g[a:b]), f"dW_up[e={e}]")
+        else:
+            assert dwd[e].abs().max().item() == 0 and dwu[e].abs().max().item() == 0
+
+
+def test_transpose_and_elementwise_lds_reads_agree(_lib):
+    """Both LDS read paths of the MN-contiguous operands give identical bits."""
+    L = _lib
+    sizes = [333, 0, 700, 64]
+    E, D, H = 4, 512, 256
+    xs, wu, wd, off = _groups(E, sizes, D, H, seed=9)
+    T = xs.shape[0]
+    g = torch.Generator().manual_seed(1)
+    gup = torch.randn(T, 2 * H, generator=g).to(torch.bfloat16).cuda()
+    off_g = torch.from_numpy(off).cuda()
+    res = []
+    for tr in (True, False):
+        L.set_lds_transpose(tr)
+        c = torch.empty(E, 2 * H, D, dtype=torch.bfloat16, device="cuda")
+        L.call("ffmoe_gemm_wgrad", gup.data_ptr(), xs.cuda().data_ptr(), off_g.data_ptr(), E, 2 * H,
+               D, c.data_ptr(), L.stream_ptr())
+        res.append(c)
+    L.set_lds_transpose(True)
+    assert torch.equal(res[0], res[1])
+
+
+# --- the whole layer against the oracle -----------------------------------------
+
+def _run_layer(x, gate, wu, wd, k, go, **kw):
+    from flashfusedmoe_amd import fused_moe
+    leaves = [t.cuda().requires_grad_(True) for t in (x, gate, wu, wd)]
+    out, losses = fused_moe(*leaves, top_k=k, **kw)
+    loss = (out.float() * go.cuda().float()).sum()
+    for key in ("aux_loss", "z_loss"):
+        if key in losses and losses[key].requires_grad:
+            loss = loss + losses[key]
+    loss.backward()
+    return out.detach().cpu(), losses, [t.grad.cpu() for t in leaves]
+
+
+@pytest.mark.parametrize("activation", ["swiglu", "geglu", "relu_squared"])
+@pytest.mark.parametrize("gating", ["softmax", "sigmoid"])
+@pytest.mark.parametrize("N,D,ffn,E,k", [(256, 128, 512, 4, 2), (1000, 256, 384, 16, 4)])
+def test_layer_forward_backward_matches_oracle(activation, gating, N, D, ffn, E, k):
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=N + E + k)
+    go = torch.randn(N, D, generator=torch.Generator().manual_seed(99)).to(torch.bfloat16)
+    aux_c, z_c = 0.01, 0.001
+    out, losses, grads = _run_layer(x, gate, wu, wd, k, go, activation=activation, gating=gating,
+                                    aux_loss_coeff=aux_c, z_loss_coeff=z_c,
+                                    allow_dropped_tokens=True)
+    # routing is pinned to the GPU's bf16 logits (identical-logits contract)
+    from flashfusedmoe_amd import ops
+    logits = ops.route(x.cuda(), gate.cuda(), None, k, 0, 1, 0.0, 0.0, False)[0].cpu()
+    ref, st = F_.forward(x, gate, wu, wd, k, activation=activation, gating=gating,
+                         allow_dropped_tokens=True, logits=logits)
+    check_close(out, ref, "output")
+    ls = F_.losses(logits, st["topk_w"], st["topk_idx"], E, gating=gating, aux_loss_coeff=aux_c,
+                   z_loss_coeff=z_c)
+    torch.testing.assert_close(losses["aux_loss"].cpu(), ls["aux_loss"].float(), rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(losses["z_loss"].cpu(), ls["z_loss"].float(), rtol=1e-4, atol=1e-6)
+    assert losses["aux_loss"].requires_grad == (gating == "sigmoid")
+
+    gr = F_.backward(st, go)
+    lg = F_.loss_grads(logits, st["topk_idx"], E, gating, aux_c, z_c).to(torch.bfloat16)
+    exp_hidden = (gr["hidden"].float() + F_.gemm(lg, gate).float())
+    exp_gate = (gr["gate"].float() + F_.gemm(lg.t().contiguous(), x).float())
+    check_close(grads[0], exp_hidden, "grad hidden")
+    check_close(grads[1], exp_gate, "grad gate", atol=2e-3 * max(1.0, exp_gate.abs().max().item()))
+    check_close(grads[2], gr["w_up"], "grad w_up")
+    check_close(grads[3], gr["w_down"], "grad w_down")
+
+
+def test_metrics_match_oracle():
+    from flashfusedmoe_amd import fused_moe
+    N, D, ffn, E, k = 640, 128, 256, 8, 2
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=3)
+    out, losses = fused_moe(*cuda(x, gate, wu, wd), top_k=k, return_metrics=True,
+                            allow_dropped_tokens=True, capacity_factor=0.5)
+    from flashfusedmoe_amd import ops
+    logits = ops.route(x.cuda(), gate.cuda(), None, k, 0, 1, 0.0, 0.0, False)[0].cpu()
+    w, idx = F_.apply_routing(logits, "softmax", k)
+    ls = F_.losses(logits, w, idx, E, return_metrics=True, capacity_factor=0.5, top_k=k)
+    assert torch.equal(losses["tokens_per_expert"].cpu(), ls["tokens_per_expert"])
+    assert losses["tokens_per_expert"].dtype == torch.int32
+    assert losses["max_expert_load"].item() == ls["max_expert_load"].item()
+    assert losses["min_expert_load"].item() == ls["min_expert_load"].item()
+    assert abs(losses["expert_load_imbalance"].item() - ls["expert_load_imbalance"].item()) < 1e-5
+    assert losses["dropped_token_count"].item() == ls["dropped_token_count"].item()
+    assert abs(losses["dropped_token_fraction"].item() - ls["dropped_token_fraction"].item()) < 1e-6
+
+
+def test_capacity_matches_oracle():
+    N, D, ffn, E, k = 512, 128, 256, 4, 2
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=21, gate_scale=0.2)
+    go = torch.randn(N, D, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    out, _, grads = _run_layer(x, gate, wu, wd, k, go, capacity_factor=1.0)
+    from flashfusedmoe_amd import ops
+    logits = ops.route(x.cuda(), gate.cuda(), None, k, 0, 1, 0.0, 0.0, False)[0].cpu()
+    ref, st = F_.forward(x, gate, wu, wd, k, capacity_factor=1.0, logits=logits)
+    assert not bool(st["keep"].all())
+    check_close(out, ref, "output")
+    gr = F_.backward(st, go)
+    check_close(grads[0], gr["hidden"], "grad hidden")
+    check_close(grads[2], gr["w_up"], "grad w_up")
+    check_close(grads[3], gr["w_down"], "grad w_down")
+
+
+def test_overflow_raises_and_alias_semantics():
+    from flashfusedmoe_amd import fused_moe
+    N, D, ffn, E, k = 64, 64, 128, 4, 1
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=42)
+    gate = gate.clone()
+    gate[0] += 1.0
+    with pytest.raises(RuntimeError, match="MoE routing overflow"):
+        fused_moe(*cuda(x, gate, wu, wd), top_k=k, max_tokens_per_expert=16)
+    out, _ = fused_moe(*cuda(x, gate, wu, wd), top_k=k, max_tokens_per_expert=16,
+                       allow_dropped_tokens=True)
+    from flashfusedmoe_amd import ops
+    logits = ops.route(x.cuda(), gate.cuda(), None, k, 0, 1, 0.0, 0.0, False)[0].cpu()
+    ref, st = F_.forward(x, gate, wu, wd, k, max_tokens_per_expert=16, allow_dropped_tokens=True,
+                         logits=logits)
+    assert not bool(st["keep"].all())
+    check_close(out.cpu(), ref, "output with overflow")
+
+
+@pytest.mark.parametrize("N,E,k", [(1, 4, 2), (4, 16, 2), (32, 4, 1), (32, 8, 3), (32, 8, 4)])
+def test_edge_cases_match_oracle(N, E, k):
+    # tests/test_production.py:488-616 analogues
+    D, ffn = 64, 128
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=N + E + k)
+    go = torch.randn(N, D, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    out, _, grads = _run_layer(x, gate, wu, wd, k, go, allow_dropped_tokens=True)
+    from flashfusedmoe_amd import ops
+    logits = ops.route(x.cuda(), gate.cuda(), None, k, 0, 1, 0.0, 0.0, False)[0].cpu()
+    ref, st = F_.forward(x, gate, wu, wd, k, allow_dropped_tokens=True, logits=logits)
+    check_close(out, ref, "output")
+    gr = F_.backward(st, go)
+    check_close(grads[0], gr["hidden"], "grad hidden")
+    check_close(grads[2], gr["w_up"], "grad w_up")
+
+
+def test_empty_experts():
+    # tests/test_production.py:502-522: experts 4..7 receive nothing
+    N, D, ffn, E, k = 16, 64, 128, 8, 2
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=7)
+    gate = gate.clone()
+    gate[4:] = 0.0
+    gate[:4] *= 100.0
+    go = torch.randn(N, D, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    out, _, grads = _run_layer(x, gate, wu, wd, k, go, allow_dropped_tokens=True)
+    from flashfusedmoe_amd import ops
+    logits = ops.route(x.cuda(), gate.cuda(), None, k, 0, 1, 0.0, 0.0, False)[0].cpu()
+    ref, st = F_.forward(x, gate, wu, wd, k, allow_dropped_tokens=True, logits=logits)
+    check_close(out, ref, "output")
+    assert grads[2][4:].abs().max().item() == 0.0
+
+
+def test_recompute_is_bitwise_identical():
+    # tests/test_production.py:258-311
+    N, D, ffn, E, k = 512, 128, 256, 8, 2
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=11)
+    go = torch.randn(N, D, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    a = _run_layer(x, gate, wu, wd, k, go, allow_dropped_tokens=True)
+    b = _run_layer(x, gate, wu, wd, k, go, allow_dropped_tokens=True, recompute_activations=True)
+    assert torch.equal(a[0], b[0])
+    for ga, gb in zip(a[2], b[2]):
+        assert torch.equal(ga, gb)
+
+
+def test_run_twice_bitwise_deterministic():
+    N, D, ffn, E, k = 2048, 256, 512, 16, 4
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=12)
+    go = torch.randn(N, D, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    a = _run_layer(x, gate, wu, wd, k, go, aux_loss_coeff=0.01, z_loss_coeff=0.001,
+                   allow_dropped_tokens=True)
+    b = _run_layer(x, gate, wu, wd, k, go, aux_loss_coeff=0.01, z_loss_coeff=0.001,
+                   allow_dropped_tokens=True)
+    assert torch.equal(a[0], b[0])
+    for ga, gb in zip(a[2], b[2]):
+        assert torch.equal(ga, gb)
+
+
+def test_expert_bias_selection_only():
+    """expert_bias shifts selection only; weights use unbiased logits
+    (fused_moe.py:163-179)."""
+    from flashfusedmoe_amd import fused_moe, ops
+    N, D, ffn, E, k = 512, 128, 256, 16, 4
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=13)
+    bias = -2.2 * torch.log(torch.randperm(E, generator=torch.Generator().manual_seed(1)).float() + 1)
+    outs = ops.route(x.cuda(), gate.cuda(), bias.cuda(), k, 0, N * k, 0.0, 0.0, False)
+    logits, idx, w = outs[0].cpu(), outs[1].cpu(), outs[2].cpu()
+    sel = logits.float() + bias
+    ridx, _ = R.topk_select(sel.numpy(), k)
+    assert np.array_equal(idx.numpy(), ridx)
+    rw = torch.softmax(logits.float().gather(1, idx), -1)
+    torch.testing.assert_close(w, rw, rtol=2e-6, atol=1e-7)
+    out, _ = fused_moe(*cuda(x, gate, wu, wd), top_k=k, expert_bias=bias.cuda(),
+                       allow_dropped_tokens=True)
+    ref, _ = F_.forward(x, gate, wu, wd, k, allow_dropped_tokens=True, logits=logits,
+                        expert_bias=bias)
+    check_close(out.cpu(), ref, "output with expert_bias")
