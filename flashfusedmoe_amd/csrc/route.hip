@@ -37,10 +37,11 @@ static inline RouteWs route_ws(void* ws, int64_t N, int E) {
   return w;
 }
 
-// Top-k insertion: keeps the KMAX best (value desc, index asc) seen so far.
-// Scanning experts in ascending order with a strict '>' keeps the lower index
-// ahead on ties, which is the reference's k-round argmax with
-// tie_break_left=True (fused_topk.py:63-70).
+// Top-k insertion: keeps the KMAX best in (value desc, index asc) order, which
+// is the reference's k-round argmax with tie_break_left=True
+// (fused_topk.py:63-70).  An element displaced from slot s still precedes an
+// equal-valued element in slot s+1 (its index is lower), so the comparison
+// is the full lexicographic one, not value alone.
 template <int KMAX>
 struct TopK {
   float v[KMAX];
@@ -56,7 +57,7 @@ struct TopK {
 #pragma unroll
     for (int s = 0; s < KMAX; ++s) {
       if (s < k) {
-        const bool take = (i[s] < 0) || (val > v[s]);
+        const bool take = (i[s] < 0) || (val > v[s]) || (val == v[s] && idx < i[s]);
         if (take) {
           const float tv = v[s];
           const int ti = i[s];

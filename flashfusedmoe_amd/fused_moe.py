@@ -143,11 +143,12 @@ class _FusedMoEFunction(torch.autograd.Function):
         aux = stats[L.STAT_AUX].clone()
         z = stats[L.STAT_Z].clone()
         ctx.aux_has_grad = gating == "sigmoid"
+        non_diff = [topk_idx, counts, stats, istats]
         if not ctx.aux_has_grad:
             # the reference's softmax aux loss has no gradient on its fused path
             # (fused_topk_routing outputs are not differentiable)
-            ctx.mark_non_differentiable(aux)
-        ctx.mark_non_differentiable(topk_idx, counts, stats, istats)
+            non_diff.append(aux)
+        ctx.mark_non_differentiable(*non_diff)
         return out, aux, z, topk_idx, counts, stats, istats
 
     @staticmethod

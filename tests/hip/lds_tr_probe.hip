@@ -20,7 +20,7 @@ __global__ void tr_probe_kernel(uint16_t* out) {
   const int row = (g >> 1) * 8 + (i >> 2);
   const int col = (g & 1) * 16 + (i & 3) * 4;
   const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(m + row * 64 + col));
-  for (int q = 0; q < 4; ++q) out[lane * 4 + q] = __builtin_bit_cast(uint16_t, v[q]);
+  reinterpret_cast<uint2*>(out)[lane] = __builtin_bit_cast(uint2, v);
 }
 
 extern "C" int ffmoe_probe_lds_tr(void* out_dev) {
