@@ -93,15 +93,16 @@ def kernel_rates(c, x, gate, wu, wd, go, reps=20):
     up_f = 2.0 * rows * D * 2 * H
     dn_f = 2.0 * rows * H * D
     b = 2  # bytes per bf16
+    tr = L.gemm_tile_rows(T, E)
     launches = {
-        "gemm_up_glu": (lambda: L.call("ffmoe_gemm_up_glu", P(xs), P(wu), P(off), P(til), E, T, D, H, 0,
-                                       P(up), P(act), st), up_f, "flop"),
-        "gemm_down": (lambda: L.call("ffmoe_gemm_down", P(act), P(wd), P(off), P(til), E, T, H, D,
+        "gemm_up_glu": (lambda: L.call("ffmoe_gemm_up_glu", P(xs), P(wu), P(off), P(til), tr, E, T, D,
+                                       H, 0, P(up), P(act), st), up_f, "flop"),
+        "gemm_down": (lambda: L.call("ffmoe_gemm_down", P(act), P(wd), P(off), P(til), tr, E, T, H, D,
                                      P(down), st), dn_f, "flop"),
         "gemm_dgrad_glu": (lambda: L.call("ffmoe_gemm_dgrad_glu", P(wgo), P(wd), P(up), P(off), P(til),
-                                          E, T, D, H, 0, P(gup), st), dn_f, "flop"),
-        "gemm_dgrad": (lambda: L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), E, T, H, D,
-                                      P(ghb), st), up_f, "flop"),
+                                          tr, E, T, D, H, 0, P(gup), st), dn_f, "flop"),
+        "gemm_dgrad": (lambda: L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), tr, E, T, H,
+                                      D, P(ghb), st), up_f, "flop"),
         "gemm_wgrad_down": (lambda: L.call("ffmoe_gemm_wgrad", P(wgo), P(act), P(off), E, D, H, P(dwd),
                                            st), dn_f, "flop"),
         "gemm_wgrad_up": (lambda: L.call("ffmoe_gemm_wgrad", P(gup), P(xs), P(off), E, 2 * H, D, P(dwu),

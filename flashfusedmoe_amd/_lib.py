@@ -36,12 +36,12 @@ SIGNATURES = {
     "ffmoe_route_fwd": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "ffmoe_route_scan": (_I, [_L, _I, _I, _I, _I, _F, _F, _I, _P, _P, _P, _P, _P, _P, _P]),
     "ffmoe_permute": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
-    "ffmoe_gemm_tile_rows": (_I, []),
+    "ffmoe_gemm_tile_rows": (_I, [_L, _I]),
     "ffmoe_set_lds_transpose": (_I, [_I]),
-    "ffmoe_gemm_up_glu": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _P, _P]),
-    "ffmoe_gemm_down": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _P, _P]),
-    "ffmoe_gemm_dgrad_glu": (_I, [_P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _P]),
-    "ffmoe_gemm_dgrad": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _P, _P]),
+    "ffmoe_gemm_up_glu": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
+    "ffmoe_gemm_down": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P]),
+    "ffmoe_gemm_dgrad_glu": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P]),
+    "ffmoe_gemm_dgrad": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P]),
     "ffmoe_gemm_wgrad": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
     "ffmoe_combine": (_I, [_P, _P, _P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_route_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I,
@@ -102,8 +102,9 @@ def call(name, *args):
     return rc
 
 
-def gemm_tile_rows():
-    return load().ffmoe_gemm_tile_rows()
+def gemm_tile_rows(max_rows, E):
+    """Row-tile height the grouped GEMMs use for max_rows rows over E experts."""
+    return load().ffmoe_gemm_tile_rows(max_rows, E)
 
 
 def route_workspace_bytes(N, E, k):

@@ -6,6 +6,12 @@
 // compact row range and tile_offsets[E+1] its first BM-row tile, so no host
 // synchronisation is needed and padding rows are never computed.
 //
+// Block = 4 waves in a 2 x 2 grid; a BM x BN block tile gives each wave a
+// (BM/2) x (BN/2) tile of 32x32 MFMA tiles (128 x 128 at BM = BN = 256: 256
+// fp32 accumulators per lane, held in AGPRs, one wave per SIMD).  The MFMA
+// operands are passed (B, A) so each lane accumulates 4 consecutive output
+// COLUMNS of one row, and the epilogue writes 8-byte packed bf16 stores.
+//
 // Operand layouts (row-major in HBM):
 //   K-contiguous  (x_sorted, act, wgo, gup as A; w_up / w_down rows as B of
 //                  the forward GEMMs) -> LDS tile [R][BK], 16-byte chunks
@@ -13,17 +19,17 @@
 //   MN-contiguous (w_down, w_up as B of the dgrad GEMMs; both operands of
 //                  the wgrad GEMMs) -> LDS tile [BK][R + pad]; fragments are
 //                  read with ds_read_b64_tr_b16 (gfx950 LDS transpose read).
+// Two LDS stages; the next stage's global loads are issued before the current
+// stage's MFMAs and land in LDS after them (one barrier per BK step).
 #include <string>
 
 #include "common.h"
 
 namespace ffmoe {
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int kThreads = 256;      // 4 waves, 2 x 2, each 64 x 64
-constexpr int MN_PAD = 16;         // elements of padding per MN-tile row
-constexpr int KC_ELEMS = 128 * BK;             // K-contiguous tile
-constexpr int MN_ELEMS = BK * (128 + MN_PAD);  // MN-contiguous tile
+constexpr int BK = 64;
+constexpr int kThreads = 256;
+constexpr int MN_PAD = 16;  // elements of padding per MN-contiguous LDS row
 
 enum Epi { EPI_STORE = 0, EPI_GLU_FWD = 1, EPI_GLU_BWD = 2 };
 
@@ -39,13 +45,12 @@ struct GemmArgs {
   const int32_t* offsets;
   const int32_t* tile_offsets;
   int E;
-  int M;  // wgrad: rows of C; grouped-rows mode: unused
-  int N;  // output columns (GLU forward: H, i.e. activation columns)
+  int M;  // wgrad: rows of C
+  int N;  // output columns (GLU forward: H, the activation columns)
   int K;  // reduction length (grouped-rows mode)
   int n_tiles;
-  int m_tiles;  // wgrad: tiles along M
+  int m_tiles;  // grouped-rows: upper bound of row tiles; wgrad: tiles along M
   int64_t total_tiles;
-  // epilogue extras
   const bf16_t* up;  // GLU backward: pre-activation [rows, 2H]
   bf16_t* C2;        // GLU forward: pre-activation out [rows, 2H] (optional)
   int H;
@@ -59,7 +64,21 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
   return (bid & 7) * per + (bid >> 3);
 }
 
-// K-contiguous tile: element (r, k) at r*BK + ((k/8) ^ (r&7))*8 + k%8.
+// Within an XCD's run, visit tiles in groups of kGroupM row tiles x all
+// column tiles, so the A rows and B columns in flight both stay few.
+constexpr int kGroupM = 4;
+__device__ __forceinline__ void grouped_order(int64_t t, int m_tiles, int n_tiles, int* mt,
+                                              int* nt) {
+  const int64_t per_group = static_cast<int64_t>(kGroupM) * n_tiles;
+  const int64_t g = t / per_group;
+  const int first = static_cast<int>(g * kGroupM);
+  const int gm = min(m_tiles - first, kGroupM);
+  const int r = static_cast<int>(t - g * per_group);
+  *mt = first + r % gm;
+  *nt = r / gm;
+}
+
+// K-contiguous tile [R][BK]: element (r, k) at r*BK + ((k/8) ^ (r&7))*8 + k%8.
 __device__ __forceinline__ int kc_off(int r, int chunk) { return r * BK + ((chunk ^ (r & 7)) << 3); }
 
 __device__ __forceinline__ bf16x8_t lds_frag_kc(const bf16_t* t, int r, int chunk) {
@@ -68,15 +87,14 @@ __device__ __forceinline__ bf16x8_t lds_frag_kc(const bf16_t* t, int r, int chun
 
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 
-// MN-contiguous tile [BK][128 + MN_PAD]: fragment for column `c0 + lane%32`
-// and k = ks*16 + (lane/32)*8 .. +8 of a 32x32x16 MFMA operand.
-template <bool TR>
+// MN-contiguous tile [BK][LD]: operand fragment for column c0 + lane%32 and
+// k = ks*16 + (lane/32)*8 .. +8 of a 32x32x16 MFMA.
+template <bool TR, int LD>
 __device__ __forceinline__ bf16x8_t lds_frag_mn(const bf16_t* t, int c0, int ks, int lane) {
-  constexpr int LD = 128 + MN_PAD;
   if constexpr (TR) {
-    // ds_read_b64_tr_b16: within each 16-lane group, lane i supplies the
-    // address of row (i/4), columns (i%4)*4..+4 of a 4 x 16 block and receives
-    // column i of it (4 consecutive rows).
+    // ds_read_b64_tr_b16: in each 16-lane group, lane i supplies the address
+    // of row i/4, columns (i%4)*4..+4 of a 4 x 16 block and receives column i
+    // of it (4 consecutive rows).
     const int g = lane >> 4, i = lane & 15;
     const int kb = ks * 16 + (g >> 1) * 8 + (i >> 2);
     const int col = c0 + (g & 1) * 16 + (i & 3) * 4;
@@ -95,40 +113,160 @@ __device__ __forceinline__ bf16x8_t lds_frag_mn(const bf16_t* t, int c0, int ks,
   }
 }
 
-// Local B-tile row -> global B row for the GLU forward: rows [0,64) are gate
-// rows a0.., rows [64,128) the matching up rows H + a0..
-__device__ __forceinline__ int glu_brow(int r, int a0, int H, bool* ok) {
-  const int a = a0 + (r & 63);
-  *ok = a < H;
-  return (r < 64) ? a : H + a;
+__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
+  return make_uint2(static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16),
+                    static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16));
 }
 
-// Column base of accumulator tile tn of wave column wn within the block tile.
-template <int EPI>
-__device__ __forceinline__ int tile_col(int wn, int tn) {
-  if constexpr (EPI == EPI_GLU_FWD) return tn * 64 + wn * 32;  // gate / up pairs
-  else return wn * 64 + tn * 32;
+__device__ __forceinline__ void unpack4(uint2 v, float* f) {
+  f[0] = __uint_as_float(v.x << 16);
+  f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16);
+  f[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
+// Transpose-read fragment from a swizzled MN-contiguous stage tile [32][R]
+// whose 16-byte chunk c of k-row k sits at chunk c ^ ((k & 3) << 2).
+template <int R>
+__device__ __forceinline__ bf16x8_t lds_frag_mn_sw(const bf16_t* t, int c0, int ks, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int kb = ks * 16 + (g >> 1) * 8 + (i >> 2);
+  const int col = c0 + (g & 1) * 16 + (i & 3) * 4;
+  const int sw = (kb & 3) << 2;  // same for rows kb and kb + 4
+  const int off = (((col >> 3) ^ sw) << 3) + (col & 7);
+  const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(t + kb * R + off));
+  const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(t + (kb + 4) * R + off));
+  return bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Stores ROWS rows of a bf16 C tile staged in LDS (row stride LDC) with the
+// block's 256 threads, 16 bytes each: plain store, GLU forward (tile columns
+// [0, BN/2) gate, [BN/2, BN) up: writes act and, if requested, the
+// pre-activation) or GLU backward (reads the pre-activation, writes its
+// gradient).  Rows are row_base + i (grouped rows, valid below row_end) or
+// m_base + i (wgrad, valid below M).
+template <int ROWS, int BN, int LDC, int MODE, int EPI>
+__device__ __forceinline__ void store_c_tile(const GemmArgs& p, const bf16_t* Cs, int e, int m_base,
+                                             int row_base, int row_end, int n0, int a0) {
+  const int tid = threadIdx.x;
+  if constexpr (EPI == EPI_GLU_FWD) {
+    constexpr int CH = BN / 16;  // 8-column chunks per half row
+    const int64_t H = p.H;
+    for (int idx = tid; idx < ROWS * CH; idx += kThreads) {
+      const int ml = idx / CH, c = (idx % CH) * 8;
+      const int64_t row = row_base + ml;
+      const int a = a0 + c;
+      if (row >= row_end || a >= p.H) continue;
+      const uint4 gv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
+      const uint4 uv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + BN / 2 + c);
+      float g[8], u[8], o[8];
+      unpack8(gv, g);
+      unpack8(uv, u);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = glu_fwd(p.act, g[i], u[i]);
+      if (p.C2 != nullptr) {
+        *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + a) = gv;
+        *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + H + a) = uv;
+      }
+      *reinterpret_cast<uint4*>(p.C + row * p.ldc + a) = pack8(o);
+    }
+  } else if constexpr (EPI == EPI_GLU_BWD) {
+    // batches of NB chunks: all pre-activation loads of a batch are issued
+    // before any of its stores (a vector-memory wait also drains earlier
+    // stores, so interleaving loads and stores would serialise them)
+    constexpr int CH = BN / 8;
+    constexpr int NB = 4;
+    static_assert((ROWS * CH) % (kThreads * NB) == 0, "whole batches");
+    const int64_t H = p.H;
+    for (int base = 0; base < ROWS * CH; base += kThreads * NB) {
+      uint4 gv[NB], uv[NB], cv[NB];
+      int64_t rowv[NB];
+      int colv[NB];
+      bool ok[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int idx = base + b * kThreads + tid;
+        const int ml = idx / CH, c = (idx % CH) * 8;
+        rowv[b] = static_cast<int64_t>(row_base) + ml;
+        colv[b] = n0 + c;
+        ok[b] = rowv[b] < row_end && colv[b] < p.N;
+        cv[b] = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
+        if (ok[b]) {
+          gv[b] = *reinterpret_cast<const uint4*>(p.up + rowv[b] * 2 * H + colv[b]);
+          uv[b] = *reinterpret_cast<const uint4*>(p.up + rowv[b] * 2 * H + H + colv[b]);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (!ok[b]) continue;
+        float ga[8], g[8], u[8], gg[8], gu[8];
+        unpack8(cv[b], ga);
+        unpack8(gv[b], g);
+        unpack8(uv[b], u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) glu_bwd(p.act, ga[i], g[i], u[i], &gg[i], &gu[i]);
+        *reinterpret_cast<uint4*>(p.C + rowv[b] * 2 * H + colv[b]) = pack8(gg);
+        *reinterpret_cast<uint4*>(p.C + rowv[b] * 2 * H + H + colv[b]) = pack8(gu);
+      }
+    }
+  } else {
+    constexpr int CH = BN / 8;
+    bf16_t* Cb = p.C;
+    if constexpr (MODE == 1) Cb += static_cast<int64_t>(e) * p.c_stride;
+    for (int idx = tid; idx < ROWS * CH; idx += kThreads) {
+      const int ml = idx / CH, c = (idx % CH) * 8;
+      const int64_t row = (MODE == 0) ? static_cast<int64_t>(row_base) + ml : static_cast<int64_t>(m_base) + ml;
+      const bool row_ok = (MODE == 0) ? row < row_end : row < p.M;
+      const int col = n0 + c;
+      if (!row_ok || col >= p.N) continue;
+      const uint4 cv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
+      if constexpr (EPI == EPI_GLU_BWD) {
+        const int64_t H = p.H;
+        float ga[8], g[8], u[8], gg[8], gu[8];
+        unpack8(cv, ga);
+        unpack8(*reinterpret_cast<const uint4*>(p.up + row * 2 * H + col), g);
+        unpack8(*reinterpret_cast<const uint4*>(p.up + row * 2 * H + H + col), u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) glu_bwd(p.act, ga[i], g[i], u[i], &gg[i], &gu[i]);
+        *reinterpret_cast<uint4*>(Cb + row * 2 * H + col) = pack8(gg);
+        *reinterpret_cast<uint4*>(Cb + row * 2 * H + H + col) = pack8(gu);
+      } else {
+        *reinterpret_cast<uint4*>(Cb + row * p.ldc + col) = cv;
+      }
+    }
+  }
+}
+
+// Register-staged kernel (fallback for K not a multiple of the direct-to-LDS
+// K step, and the element-wise LDS read variant used to cross-check the
+// transpose reads).
 // MODE 0: grouped rows (A rows = expert rows, B per expert).
 // MODE 1: grouped K (wgrad): reduction over an expert's rows.
-template <bool A_KC, bool B_KC, int MODE, int EPI, bool TR>
-__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * ((A_KC ? KC_ELEMS : MN_ELEMS) +
-                                                           (B_KC ? KC_ELEMS : MN_ELEMS))];
-  constexpr int A_ELEMS = A_KC ? KC_ELEMS : MN_ELEMS;
-  constexpr int B_ELEMS = B_KC ? KC_ELEMS : MN_ELEMS;
-  constexpr int LDMN = 128 + MN_PAD;
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI, bool TR>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
+  constexpr int WM = BM / 2, WN = BN / 2;   // per-wave tile
+  constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA tiles per wave
+  constexpr int LDA = BM + MN_PAD, LDB = BN + MN_PAD;
+  constexpr int A_ELEMS = A_KC ? BM * BK : BK * LDA;
+  constexpr int B_ELEMS = B_KC ? BN * BK : BK * LDB;
+  constexpr int STAGE = A_ELEMS + B_ELEMS;
+  constexpr int LDC = BN + 8;  // C tile row stride in LDS (elements)
+  constexpr int SMEM = (2 * STAGE > BM * LDC) ? 2 * STAGE : BM * LDC;
+  constexpr int A_LOADS = BM / 32;  // 16-byte chunks per thread per stage
+  constexpr int B_LOADS = BN / 32;
+  static_assert(EPI != EPI_GLU_FWD || (TN % 2 == 0), "GLU forward pairs gate/up tiles");
+  __shared__ __attribute__((aligned(16))) bf16_t smem[SMEM];
 
   const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
   if (tile >= p.total_tiles) return;
 
   // ---- tile decode ----
-  int e, m0, n0;
+  int e, m0 = 0, n0;
   int row_begin = 0, row_end = 0;  // MODE 0: A rows; MODE 1: K range
   if constexpr (MODE == 0) {
-    const int mt = static_cast<int>(tile / p.n_tiles);
-    n0 = static_cast<int>(tile % p.n_tiles) * BN;
+    int mt, nt;
+    grouped_order(tile, p.m_tiles, p.n_tiles, &mt, &nt);
+    n0 = nt * BN;
     if (mt >= p.tile_offsets[p.E]) return;
     int lo = 0, hi = p.E - 1;  // last e with tile_offsets[e] <= mt
     while (lo < hi) {
@@ -138,13 +276,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs p) {
     e = lo;
     row_begin = p.offsets[e] + (mt - p.tile_offsets[e]) * BM;
     row_end = p.offsets[e + 1];
-    m0 = 0;
   } else {
     const int64_t per_e = static_cast<int64_t>(p.m_tiles) * p.n_tiles;
     e = static_cast<int>(tile / per_e);
-    const int64_t r = tile % per_e;
-    m0 = static_cast<int>(r / p.n_tiles) * BM;
-    n0 = static_cast<int>(r % p.n_tiles) * BN;
+    int mt, nt;
+    grouped_order(tile - static_cast<int64_t>(e) * per_e, p.m_tiles, p.n_tiles, &mt, &nt);
+    m0 = mt * BM;
+    n0 = nt * BN;
     row_begin = p.offsets[e];
     row_end = p.offsets[e + 1];
   }
@@ -157,24 +295,30 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs p) {
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // buffer b: A tile at smem + b*(A_ELEMS+B_ELEMS), B tile right after it
-  auto a_tile = [&](int b) { return smem + b * (A_ELEMS + B_ELEMS); };
-  auto b_tile = [&](int b) { return smem + b * (A_ELEMS + B_ELEMS) + A_ELEMS; };
+  auto a_tile = [&](int b) { return smem + b * STAGE; };
+  auto b_tile = [&](int b) { return smem + b * STAGE + A_ELEMS; };
+  // column base (within the block tile) of accumulator tile tn of this wave
+  auto tile_col = [&](int tn) {
+    if constexpr (EPI == EPI_GLU_FWD)
+      return (tn < TN / 2) ? wn * (WN / 2) + tn * 32 : BN / 2 + wn * (WN / 2) + (tn - TN / 2) * 32;
+    else
+      return wn * WN + tn * 32;
+  };
 
-  uint4 ra[4], rb[4];
+  uint4 ra[A_LOADS], rb[B_LOADS];
 
   auto load_a = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < A_LOADS; ++i) {
       const int c = tid + kThreads * i;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if constexpr (A_KC) {  // MODE 0 only: tile [128 rows][BK]
+      if constexpr (A_KC) {  // MODE 0: tile [BM rows][BK]
         const int r = c >> 3, kc = c & 7;
         const int grow = row_begin + r;
         const int kk = k0 + kc * 8;
         if (grow < row_end && kk < K) v = *reinterpret_cast<const uint4*>(p.A + grow * p.lda + kk);
-      } else {  // MODE 1: tile [BK][128 cols of M]
-        const int kr = c >> 4, rc = c & 15;
+      } else {  // MODE 1: tile [BK][BM columns of M]
+        const int kr = c / (BM / 8), rc = c % (BM / 8);
         const int grow = row_begin + k0 + kr;
         const int m = m0 + rc * 8;
         if (grow < row_end && m < p.M) v = *reinterpret_cast<const uint4*>(p.A + grow * p.lda + m);
@@ -184,7 +328,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs p) {
   };
   auto load_b = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < B_LOADS; ++i) {
       const int c = tid + kThreads * i;
       uint4 v = make_uint4(0, 0, 0, 0);
       if constexpr (B_KC) {  // MODE 0 NT: B [N rows][K]
@@ -193,19 +337,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs p) {
         bool ok;
         int brow;
         if constexpr (EPI == EPI_GLU_FWD) {
-          brow = glu_brow(r, a0, p.H, &ok);
+          // rows [0, BN/2): gate rows a0.., rows [BN/2, BN): up rows H + a0..
+          const int a = a0 + (r % (BN / 2));
+          ok = a < p.H;
+          brow = (r < BN / 2) ? a : p.H + a;
         } else {
           brow = n0 + r;
           ok = brow < p.N;
         }
         if (ok && kk < K) v = *reinterpret_cast<const uint4*>(Be + static_cast<int64_t>(brow) * p.ldb + kk);
       } else if constexpr (MODE == 0) {  // NN: B [K rows][N]
-        const int kr = c >> 4, rc = c & 15;
+        const int kr = c / (BN / 8), rc = c % (BN / 8);
         const int kk = k0 + kr;
         const int n = n0 + rc * 8;
         if (kk < K && n < p.N) v = *reinterpret_cast<const uint4*>(Be + static_cast<int64_t>(kk) * p.ldb + n);
       } else {  // wgrad: B [rows][N]
-        const int kr = c >> 4, rc = c & 15;
+        const int kr = c / (BN / 8), rc = c % (BN / 8);
         const int grow = row_begin + k0 + kr;
         const int n = n0 + rc * 8;
         if (grow < row_end && n < p.N) v = *reinterpret_cast<const uint4*>(Be + grow * p.ldb + n);
@@ -215,26 +362,28 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs p) {
   };
   auto store_tiles = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < A_LOADS; ++i) {
       const int c = tid + kThreads * i;
-      if constexpr (A_KC) {
+      if constexpr (A_KC)
         *reinterpret_cast<uint4*>(a_tile(buf) + kc_off(c >> 3, c & 7)) = ra[i];
-      } else {
-        *reinterpret_cast<uint4*>(a_tile(buf) + (c >> 4) * LDMN + (c & 15) * 8) = ra[i];
-      }
-      if constexpr (B_KC) {
+      else
+        *reinterpret_cast<uint4*>(a_tile(buf) + (c / (BM / 8)) * LDA + (c % (BM / 8)) * 8) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+      const int c = tid + kThreads * i;
+      if constexpr (B_KC)
         *reinterpret_cast<uint4*>(b_tile(buf) + kc_off(c >> 3, c & 7)) = rb[i];
-      } else {
-        *reinterpret_cast<uint4*>(b_tile(buf) + (c >> 4) * LDMN + (c & 15) * 8) = rb[i];
-      }
+      else
+        *reinterpret_cast<uint4*>(b_tile(buf) + (c / (BN / 8)) * LDB + (c % (BN / 8)) * 8) = rb[i];
     }
   };
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
@@ -254,24 +403,26 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs p) {
       const bf16_t* bt = b_tile(cur);
 #pragma unroll
       for (int ks = 0; ks < BK / 16; ++ks) {
-        bf16x8_t af[2], bfr[2];
+        bf16x8_t af[TM], bfr[TN];
 #pragma unroll
-        for (int tm = 0; tm < 2; ++tm) {
-          const int r0 = wm * 64 + tm * 32;
+        for (int tm = 0; tm < TM; ++tm) {
+          const int r0 = wm * WM + tm * 32;
           if constexpr (A_KC) af[tm] = lds_frag_kc(at, r0 + (lane & 31), ks * 2 + (lane >> 5));
-          else af[tm] = lds_frag_mn<TR>(at, r0, ks, lane);
+          else af[tm] = lds_frag_mn<TR, LDA>(at, r0, ks, lane);
         }
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn) {
-          const int c0 = tile_col<EPI>(wn, tn);
+        for (int tn = 0; tn < TN; ++tn) {
+          const int c0 = tile_col(tn);
           if constexpr (B_KC) bfr[tn] = lds_frag_kc(bt, c0 + (lane & 31), ks * 2 + (lane >> 5));
-          else bfr[tn] = lds_frag_mn<TR>(bt, c0, ks, lane);
+          else bfr[tn] = lds_frag_mn<TR, LDB>(bt, c0, ks, lane);
         }
+        // (B, A) operand order: lane l accumulates row l%32 of the tile and
+        // columns 8*(r/4) + 4*(l/32) + r%4.
 #pragma unroll
-        for (int tm = 0; tm < 2; ++tm)
+        for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-          for (int tn = 0; tn < 2; ++tn)
-            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bfr[tn], acc[tm][tn], 0, 0, 0);
+          for (int tn = 0; tn < TN; ++tn)
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[tn], af[tm], acc[tm][tn], 0, 0, 0);
       }
       if (kt + 1 < nk) store_tiles(cur ^ 1);
       __syncthreads();
@@ -279,90 +430,392 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs p) {
   }
 
   // ---- epilogue ----
-  // 32x32 accumulator layout: acc[r] of lane l is row (r/4)*8 + (l/32)*4 + r%4,
-  // column l%32 of the 32x32 tile.
-  const int lc = lane & 31;
+  // 1) every lane writes its accumulators, rounded to bf16, into a C tile in
+  //    LDS (the pipeline buffers are free after the loop's last barrier);
+  //    lane l holds row l%32 and columns 8*(r/4) + 4*(l/32) + r%4 of each
+  //    32x32 tile: 4 consecutive columns -> one 8-byte LDS write.
+  // 2) the block reads the tile back in 16-byte row chunks and applies the
+  //    epilogue op with coalesced 16-byte global loads and stores.
+  bf16_t* Cs = smem;
+  {
+    const int lr = lane & 31;
+    const int lq = (lane >> 5) * 4;
 #pragma unroll
-  for (int tm = 0; tm < 2; ++tm) {
+    for (int tm = 0; tm < TM; ++tm) {
+      const int ml = wm * WM + tm * 32 + lr;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lr = wm * 64 + tm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-      if constexpr (MODE == 0) {
-        const int grow = row_begin + lr;
-        if (grow >= row_end) continue;
-        if constexpr (EPI == EPI_GLU_FWD) {
-          const int a = a0 + wn * 32 + lc;
-          if (a >= p.H) continue;
-          const bf16_t gh = f32_to_bf16(acc[tm][0][r]);
-          const bf16_t uh = f32_to_bf16(acc[tm][1][r]);
-          if (p.C2 != nullptr) {
-            p.C2[grow * (2 * static_cast<int64_t>(p.H)) + a] = gh;
-            p.C2[grow * (2 * static_cast<int64_t>(p.H)) + p.H + a] = uh;
-          }
-          p.C[grow * p.ldc + a] = f32_to_bf16(glu_fwd(p.act, bf16_to_f32(gh), bf16_to_f32(uh)));
-        } else {
+      for (int tn = 0; tn < TN; ++tn) {
+        const int nl = tile_col(tn) + lq;
 #pragma unroll
-          for (int tn = 0; tn < 2; ++tn) {
-            const int col = n0 + tile_col<EPI>(wn, tn) + lc;
-            if (col >= p.N) continue;
-            if constexpr (EPI == EPI_GLU_BWD) {
-              const float ga = round_bf16(acc[tm][tn][r]);
-              const int64_t ub = grow * (2 * static_cast<int64_t>(p.H));
-              const float g = bf16_to_f32(p.up[ub + col]);
-              const float u = bf16_to_f32(p.up[ub + p.H + col]);
-              float gg, gu;
-              glu_bwd(p.act, ga, g, u, &gg, &gu);
-              p.C[ub + col] = f32_to_bf16(gg);
-              p.C[ub + p.H + col] = f32_to_bf16(gu);
-            } else {
-              p.C[grow * p.ldc + col] = f32_to_bf16(acc[tm][tn][r]);
-            }
-          }
-        }
-      } else {
-        const int m = m0 + lr;
-        if (m >= p.M) continue;
-        bf16_t* Ce = p.C + static_cast<int64_t>(e) * p.c_stride;
-#pragma unroll
-        for (int tn = 0; tn < 2; ++tn) {
-          const int col = n0 + tile_col<EPI>(wn, tn) + lc;
-          if (col < p.N) Ce[static_cast<int64_t>(m) * p.ldc + col] = f32_to_bf16(acc[tm][tn][r]);
+        for (int q = 0; q < 4; ++q) {
+          *reinterpret_cast<uint2*>(Cs + ml * LDC + nl + q * 8) =
+              pack4(acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
+                    acc[tm][tn][4 * q + 3]);
         }
       }
     }
   }
+  __syncthreads();
+  store_c_tile<BM, BN, LDC, MODE, EPI>(p, Cs, e, m0, row_begin, row_end, n0, a0);
 }
 
-template <bool A_KC, bool B_KC, int MODE, int EPI>
+// ---------------------------------------------------------------------------
+// Direct-to-LDS pipeline (the main path): BK = 32, a ring of kStages LDS
+// stages filled by buffer_load_dwordx4 ... lds (each wave instruction writes
+// 1 KiB of consecutive LDS; per-lane source addresses implement the swizzle;
+// out-of-range rows read as zero through the buffer descriptor's bounds).
+//   K-contiguous stage tile [R][32]: 16-byte chunk c of row r stored at
+//     chunk c ^ ((r >> 2) & 3): the 16 rows one ds_read_b128 cycle serves hit
+//     16 distinct 16-byte bank slots (64 banks x 4 bytes).
+//   MN-contiguous stage tile [32][R]: chunk c of k-row k stored at
+//     c ^ ((k & 3) << 2): the 2 x 4 rows x 32 bytes of one transpose-read
+//     cycle hit distinct bank slots.
+// Each K step: wait for this stage's loads (s_waitcnt vmcnt), one s_barrier,
+// issue the loads of the stage kStages-1 ahead into the buffer freed by the
+// previous step, then the MFMAs.
+// ---------------------------------------------------------------------------
+constexpr int DL_BK = 32;
+constexpr int kStages = 4;
+
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+  // s_waitcnt with only the vector-memory count constrained (expcnt and
+  // lgkmcnt at their maxima); n is one of a few small constants
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    case 16: __builtin_amdgcn_s_waitcnt(0x4F70); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+// The body is a __device__ function (the buffer-descriptor type exists only
+// in the device pass); gemm_dl_kernel below is the launchable wrapper.
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
+__device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_EL = BM * DL_BK, B_EL = BN * DL_BK;  // elements per stage tile
+  constexpr int STAGE = A_EL + B_EL;
+  constexpr int LA = BM / 64, LB = BN / 64;  // 16-byte loads per thread per stage
+  constexpr int LDC = BN + 8;                // C staging row stride
+  constexpr int SMEM = (kStages * STAGE > BM * LDC) ? kStages * STAGE : BM * LDC;
+  static_assert(EPI != EPI_GLU_FWD || (TN % 2 == 0), "GLU forward pairs gate/up tiles");
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[SMEM];
+
+  const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
+  if (tile >= p.total_tiles) return;
+
+  int e, m0 = 0, n0;
+  int row_begin = 0, row_end = 0;
+  if constexpr (MODE == 0) {
+    int mt, nt;
+    grouped_order(tile, p.m_tiles, p.n_tiles, &mt, &nt);
+    n0 = nt * BN;
+    if (mt >= p.tile_offsets[p.E]) return;
+    int lo = 0, hi = p.E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.tile_offsets[mid] <= mt) lo = mid; else hi = mid - 1;
+    }
+    e = lo;
+    row_begin = p.offsets[e] + (mt - p.tile_offsets[e]) * BM;
+    row_end = p.offsets[e + 1];
+  } else {
+    const int64_t per_e = static_cast<int64_t>(p.m_tiles) * p.n_tiles;
+    e = static_cast<int>(tile / per_e);
+    int mt, nt;
+    grouped_order(tile - static_cast<int64_t>(e) * per_e, p.m_tiles, p.n_tiles, &mt, &nt);
+    m0 = mt * BM;
+    n0 = nt * BN;
+    row_begin = p.offsets[e];
+    row_end = p.offsets[e + 1];
+  }
+  const int K = (MODE == 0) ? p.K : (row_end - row_begin);
+  const int a0 = (EPI == EPI_GLU_FWD) ? n0 / 2 : 0;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // buffer descriptors: reads outside [base, base + bytes) return zero
+  __amdgpu_buffer_rsrc_t ra, rb;
+  if constexpr (MODE == 0) {
+    const int rows = min(row_end - row_begin, BM);
+    ra = make_rsrc(p.A + static_cast<int64_t>(row_begin) * p.lda,
+                   static_cast<uint32_t>(rows * p.lda * 2));
+    const bf16_t* Be = p.B + static_cast<int64_t>(e) * p.b_stride;
+    const int64_t brows = B_KC ? ((EPI == EPI_GLU_FWD) ? 2 * static_cast<int64_t>(p.H) : p.N) : p.K;
+    rb = make_rsrc(Be, static_cast<uint32_t>(brows * p.ldb * 2));
+  } else {
+    const int64_t rows = row_end - row_begin;
+    ra = make_rsrc(p.A + static_cast<int64_t>(row_begin) * p.lda, static_cast<uint32_t>(rows * p.lda * 2));
+    rb = make_rsrc(p.B + static_cast<int64_t>(row_begin) * p.ldb, static_cast<uint32_t>(rows * p.ldb * 2));
+  }
+
+  // per-thread byte offsets of its stage-0 chunks (the k step adds a stride)
+  uint32_t offa[LA], offb[LB];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int pos = i * kThreads + tid;
+    if constexpr (A_KC) {
+      const int r = pos >> 2, c = (pos & 3) ^ ((r >> 2) & 3);
+      offa[i] = static_cast<uint32_t>((r * p.lda + c * 8) * 2);
+    } else {
+      const int k = pos / (BM / 8), c = (pos % (BM / 8)) ^ ((k & 3) << 2);
+      offa[i] = static_cast<uint32_t>((k * p.lda + m0 + c * 8) * 2);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < LB; ++i) {
+    const int pos = i * kThreads + tid;
+    if constexpr (B_KC) {
+      const int r = pos >> 2, c = (pos & 3) ^ ((r >> 2) & 3);
+      int brow;
+      if constexpr (EPI == EPI_GLU_FWD) {
+        const int a = a0 + (r % (BN / 2));
+        brow = (r < BN / 2) ? a : p.H + a;
+      } else {
+        brow = n0 + r;
+      }
+      offb[i] = static_cast<uint32_t>((static_cast<int64_t>(brow) * p.ldb + c * 8) * 2);
+    } else {
+      const int k = pos / (BN / 8), c = (pos % (BN / 8)) ^ ((k & 3) << 2);
+      offb[i] = static_cast<uint32_t>((k * p.ldb + n0 + c * 8) * 2);
+    }
+  }
+  // byte advance of one K step
+  const uint32_t stepa = A_KC ? DL_BK * 2 : static_cast<uint32_t>(DL_BK * p.lda * 2);
+  const uint32_t stepb = B_KC ? DL_BK * 2 : static_cast<uint32_t>(DL_BK * p.ldb * 2);
+
+  const int nk = (K + DL_BK - 1) / DL_BK;
+  // Loads of K step `kstep` into stage buffer `buf`.  Steps past the end are
+  // still issued, with an out-of-range offset (the buffer returns zeros and
+  // moves no memory), so every step has the same number of loads in flight.
+  auto issue = [&](int kstep, int buf) {
+    bf16_t* at = smem + buf * STAGE;
+    bf16_t* bt = at + A_EL;
+    const bool live = kstep < nk;
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (lds_void_t*)(at + (i * kThreads + wave * 64) * 8), 16,
+          live ? offa[i] + kstep * stepa : 0xFFFFFFF0u, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < LB; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, (lds_void_t*)(bt + (i * kThreads + wave * 64) * 8), 16,
+          live ? offb[i] + kstep * stepb : 0xFFFFFFF0u, 0, 0, 0);
+  };
+
+  auto tile_col = [&](int tn) {
+    if constexpr (EPI == EPI_GLU_FWD)
+      return (tn < TN / 2) ? wn * (WN / 2) + tn * 32 : BN / 2 + wn * (WN / 2) + (tn - TN / 2) * 32;
+    else
+      return wn * WN + tn * 32;
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  static_assert(DL_BK == 32, "two MFMA k-steps per stage");
+  // MFMA operand fragments of one k-step (16 of K), double-buffered in
+  // registers: set 0 holds k-step 0 of a stage, set 1 k-step 1.  The reads of
+  // one set overlap the MFMAs of the other; k-step 0 of stage kt+1 is read
+  // right after the barrier that publishes it, during k-step 1's MFMAs.
+  bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  auto read_ks = [&](int buf, int ks, bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) {
+    const bf16_t* at = smem + buf * STAGE;
+    const bf16_t* bt = at + A_EL;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      const int r0 = wm * WM + tm * 32;
+      if constexpr (A_KC) {
+        const int r = r0 + (lane & 31);
+        const int c = (ks * 2 + (lane >> 5)) ^ ((r >> 2) & 3);
+        fa[tm] = *reinterpret_cast<const bf16x8_t*>(at + r * DL_BK + c * 8);
+      } else {
+        fa[tm] = lds_frag_mn_sw<BM>(at, r0, ks, lane);
+      }
+    }
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int c0 = tile_col(tn);
+      if constexpr (B_KC) {
+        const int r = c0 + (lane & 31);
+        const int c = (ks * 2 + (lane >> 5)) ^ ((r >> 2) & 3);
+        fb[tn] = *reinterpret_cast<const bf16x8_t*>(bt + r * DL_BK + c * 8);
+      } else {
+        fb[tn] = lds_frag_mn_sw<BN>(bt, c0, ks, lane);
+      }
+    }
+  };
+  auto mfma_ks = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[TN]) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[tn], fa[tm], acc[tm][tn], 0, 0, 0);
+  };
+  // LDS fragment reads per k-step (a transpose-read fragment takes two)
+  constexpr int NR = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);
+  constexpr int NM = TM * TN;  // MFMAs per k-step
+  // Stages in flight: before the barrier of step kt, steps up to kt+kStages-1
+  // have been issued and step kt+1 must have landed, so kStages-2 steps of
+  // loads may stay outstanding: s_waitcnt vmcnt(that) and lgkmcnt(0).
+  constexpr int kInFlight = (kStages - 2) * (LA + LB);
+  constexpr int kWaitLoads = (kInFlight & 15) | ((kInFlight >> 4) << 14) | 0x70 | 0xF00;
+  constexpr int kWaitLoadsLds = (kInFlight & 15) | ((kInFlight >> 4) << 14) | 0x70;
+  static_assert(kInFlight < 64, "vmcnt range");
+
+  // Scheduling of one k-step region: pair each LDS read and each stage load
+  // with an MFMA, so one wave per SIMD issues them in the MFMAs' shadow.
+  auto interleave = [&](int nvmem) {
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // MFMA
+      if (i < nvmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+      if (i < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // DS read
+    }
+  };
+
+  if (nk > 0) {
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s) issue(s, s);
+    __builtin_amdgcn_s_waitcnt(kWaitLoads);  // stage 0 landed
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(kStages - 1, kStages - 1);
+    read_ks(0, 0, fa0, fb0);
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      // k-step 1 of stage kt: fragments read while k-step 0 runs
+      read_ks(kt & (kStages - 1), 1, fa1, fb1);
+      mfma_ks(fa0, fb0);
+      interleave(0);
+      // publish stage kt+1 (and retire this wave's reads of stage kt)
+      __builtin_amdgcn_s_waitcnt(kWaitLoadsLds);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      // refill stage kt's buffer, read k-step 0 of stage kt+1, run k-step 1
+      issue(kt + kStages, kt & (kStages - 1));
+      read_ks((kt + 1) & (kStages - 1), 0, fa0, fb0);
+      mfma_ks(fa1, fb1);
+      interleave(LA + LB);
+    }
+    read_ks((nk - 1) & (kStages - 1), 1, fa1, fb1);
+    mfma_ks(fa0, fb0);
+    mfma_ks(fa1, fb1);
+  }
+  wait_vmcnt_le(0);
+  __syncthreads();
+
+  // epilogue: every wave stages its bf16 accumulators in the LDS C tile (one
+  // 32x32 MFMA tile at a time; the scheduling barriers keep the compiler from
+  // hoisting all accumulator reads, which would spill), then the block stores
+  // the whole tile
+  bf16_t* Cs = smem;
+  const int lr = lane & 31;
+  const int lq = (lane >> 5) * 4;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+    const int ml = wm * WM + tm * 32 + lr;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int nl = tile_col(tn) + lq;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<uint2*>(Cs + ml * LDC + nl + q * 8) =
+            pack4(acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
+                  acc[tm][tn][4 * q + 3]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();
+  store_c_tile<BM, BN, LDC, MODE, EPI>(p, Cs, e, m0, row_begin, row_end, n0, a0);
+}
+
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
+  gemm_dl_body<BM, BN, A_KC, B_KC, MODE, EPI>(p);
+}
+
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
 static int launch(const GemmArgs& a, hipStream_t st, const char* name) {
   if (a.total_tiles <= 0) return clear_error();
   const int64_t grid = (a.total_tiles + 7) / 8 * 8;
   if (grid > 0x7fffffff) return set_error(std::string(name) + ": problem too large");
-  if (g_use_tr)
-    hipLaunchKernelGGL((gemm_kernel<A_KC, B_KC, MODE, EPI, true>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kThreads), 0, st, a);
+  // the direct-to-LDS pipeline needs whole K steps (grouped-rows mode) and the
+  // transpose-read path; everything else takes the register-staged kernel
+  const bool dl = g_use_tr && (MODE == 1 || a.K % DL_BK == 0);
+  if (dl)
+    hipLaunchKernelGGL((gemm_dl_kernel<BM, BN, A_KC, B_KC, MODE, EPI>),
+                       dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, st, a);
+  else if (g_use_tr)
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, A_KC, B_KC, MODE, EPI, true>),
+                       dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((gemm_kernel<A_KC, B_KC, MODE, EPI, false>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, A_KC, B_KC, MODE, EPI, false>),
+                       dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, st, a);
   if (check_launch(name)) return 1;
   return clear_error();
 }
 
-static GemmArgs base_args(const int32_t* offsets, const int32_t* tile_offsets, int E) {
+// Grouped-rows launch with the row-tile height the caller's tile_offsets were
+// computed for.
+template <int BN, bool B_KC, int EPI>
+static int launch_rows(const GemmArgs& a, int tile_rows, hipStream_t st, const char* name) {
+  if (tile_rows == 256) return launch<256, BN, true, B_KC, 0, EPI>(a, st, name);
+  return launch<128, BN, true, B_KC, 0, EPI>(a, st, name);
+}
+
+static GemmArgs rows_args(const int32_t* offsets, const int32_t* tile_offsets, int E,
+                          int64_t max_rows, int tile_rows, int n_tiles) {
   GemmArgs a{};
   a.offsets = offsets;
   a.tile_offsets = tile_offsets;
   a.E = E;
+  a.n_tiles = n_tiles;
+  a.m_tiles = static_cast<int>((max_rows + tile_rows - 1) / tile_rows + E);
+  a.total_tiles = static_cast<int64_t>(a.m_tiles) * n_tiles;
   return a;
 }
 
-static int64_t row_tiles_bound(int64_t max_rows, int E) { return (max_rows + BM - 1) / BM + E; }
+static int check_rows(const char* name, int E, int64_t max_rows, int D, int H, int tile_rows) {
+  if (E < 1 || E > FFMOE_MAX_EXPERTS || D <= 0 || D % 8 != 0 || H <= 0 || H % 8 != 0 || max_rows < 0)
+    return set_error(std::string(name) + ": D and H must be positive multiples of 8");
+  if (tile_rows != 128 && tile_rows != 256)
+    return set_error(std::string(name) + ": tile_rows must be 128 or 256");
+  return 0;
+}
 
 }  // namespace ffmoe
 
 using namespace ffmoe;
 
-extern "C" int ffmoe_gemm_tile_rows(void) { return BM; }
+extern "C" int ffmoe_gemm_tile_rows(int64_t max_rows, int E) {
+  // 256-row tiles once experts average at least 384 rows; 128 below, where a
+  // half-empty 256-row tail tile would waste more than the bigger tile saves.
+  return (E > 0 && max_rows / E >= 384) ? 256 : 128;
+}
 
 extern "C" int ffmoe_set_lds_transpose(int enable) {
   const int prev = g_use_tr;
@@ -371,12 +824,13 @@ extern "C" int ffmoe_set_lds_transpose(int enable) {
 }
 
 extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const int32_t* offsets,
-                                 const int32_t* tile_offsets, int E, int64_t max_rows, int D, int H,
-                                 int activation, void* up_out, void* act_out, void* stream) {
-  if (E < 1 || E > FFMOE_MAX_EXPERTS || D <= 0 || D % 8 != 0 || H <= 0 || H % 8 != 0 || max_rows < 0)
-    return set_error("ffmoe_gemm_up_glu: D and H must be positive multiples of 8");
+                                 const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                                 int D, int H, int activation, void* up_out, void* act_out,
+                                 void* stream) {
+  if (check_rows("ffmoe_gemm_up_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > 2) return set_error("ffmoe_gemm_up_glu: unknown activation");
-  GemmArgs a = base_args(offsets, tile_offsets, E);
+  constexpr int BN = 256;
+  GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BN / 2 - 1) / (BN / 2));
   a.A = static_cast<const bf16_t*>(x_sorted);
   a.B = static_cast<const bf16_t*>(w_up);
   a.C = static_cast<bf16_t*>(act_out);
@@ -389,17 +843,15 @@ extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const i
   a.K = D;
   a.H = H;
   a.act = activation;
-  a.n_tiles = (H + 63) / 64;
-  a.total_tiles = row_tiles_bound(max_rows, E) * a.n_tiles;
-  return launch<true, true, 0, EPI_GLU_FWD>(a, static_cast<hipStream_t>(stream), "gemm_up_glu");
+  return launch_rows<BN, true, EPI_GLU_FWD>(a, tile_rows, static_cast<hipStream_t>(stream), "gemm_up_glu");
 }
 
 extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
-                               const int32_t* tile_offsets, int E, int64_t max_rows, int H, int D,
-                               void* down_out, void* stream) {
-  if (E < 1 || E > FFMOE_MAX_EXPERTS || D <= 0 || D % 8 != 0 || H <= 0 || H % 8 != 0 || max_rows < 0)
-    return set_error("ffmoe_gemm_down: D and H must be positive multiples of 8");
-  GemmArgs a = base_args(offsets, tile_offsets, E);
+                               const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                               int H, int D, void* down_out, void* stream) {
+  if (check_rows("ffmoe_gemm_down", E, max_rows, D, H, tile_rows)) return 1;
+  constexpr int BN = 256;
+  GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(act);
   a.B = static_cast<const bf16_t*>(w_down);
   a.C = static_cast<bf16_t*>(down_out);
@@ -409,19 +861,17 @@ extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_
   a.b_stride = static_cast<int64_t>(D) * H;
   a.N = D;
   a.K = H;
-  a.n_tiles = (D + BN - 1) / BN;
-  a.total_tiles = row_tiles_bound(max_rows, E) * a.n_tiles;
-  return launch<true, true, 0, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_down");
+  return launch_rows<BN, true, EPI_STORE>(a, tile_rows, static_cast<hipStream_t>(stream), "gemm_down");
 }
 
 extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,
-                                    const int32_t* offsets, const int32_t* tile_offsets, int E,
-                                    int64_t max_rows, int D, int H, int activation, void* gup_out,
-                                    void* stream) {
-  if (E < 1 || E > FFMOE_MAX_EXPERTS || D <= 0 || D % 8 != 0 || H <= 0 || H % 8 != 0 || max_rows < 0)
-    return set_error("ffmoe_gemm_dgrad_glu: D and H must be positive multiples of 8");
+                                    const int32_t* offsets, const int32_t* tile_offsets,
+                                    int tile_rows, int E, int64_t max_rows, int D, int H,
+                                    int activation, void* gup_out, void* stream) {
+  if (check_rows("ffmoe_gemm_dgrad_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > 2) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
-  GemmArgs a = base_args(offsets, tile_offsets, E);
+  constexpr int BN = 256;
+  GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(wgo);
   a.B = static_cast<const bf16_t*>(w_down);
   a.C = static_cast<bf16_t*>(gup_out);
@@ -434,17 +884,16 @@ extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const v
   a.K = D;
   a.H = H;
   a.act = activation;
-  a.n_tiles = (H + BN - 1) / BN;
-  a.total_tiles = row_tiles_bound(max_rows, E) * a.n_tiles;
-  return launch<true, false, 0, EPI_GLU_BWD>(a, static_cast<hipStream_t>(stream), "gemm_dgrad_glu");
+  return launch_rows<BN, false, EPI_GLU_BWD>(a, tile_rows, static_cast<hipStream_t>(stream),
+                                             "gemm_dgrad_glu");
 }
 
 extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t* offsets,
-                                const int32_t* tile_offsets, int E, int64_t max_rows, int H, int D,
-                                void* ghb_out, void* stream) {
-  if (E < 1 || E > FFMOE_MAX_EXPERTS || D <= 0 || D % 8 != 0 || H <= 0 || H % 8 != 0 || max_rows < 0)
-    return set_error("ffmoe_gemm_dgrad: D and H must be positive multiples of 8");
-  GemmArgs a = base_args(offsets, tile_offsets, E);
+                                const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                                int H, int D, void* ghb_out, void* stream) {
+  if (check_rows("ffmoe_gemm_dgrad", E, max_rows, D, H, tile_rows)) return 1;
+  constexpr int BN = 256;
+  GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(gup);
   a.B = static_cast<const bf16_t*>(w_up);
   a.C = static_cast<bf16_t*>(ghb_out);
@@ -454,16 +903,17 @@ extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t
   a.b_stride = static_cast<int64_t>(2) * H * D;
   a.N = D;
   a.K = 2 * H;
-  a.n_tiles = (D + BN - 1) / BN;
-  a.total_tiles = row_tiles_bound(max_rows, E) * a.n_tiles;
-  return launch<true, false, 0, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_dgrad");
+  return launch_rows<BN, false, EPI_STORE>(a, tile_rows, static_cast<hipStream_t>(stream), "gemm_dgrad");
 }
 
 extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
                                 int Nc, void* c_out, void* stream) {
   if (E < 1 || M <= 0 || M % 8 != 0 || Nc <= 0 || Nc % 8 != 0)
     return set_error("ffmoe_gemm_wgrad: M and Nc must be positive multiples of 8");
-  GemmArgs a = base_args(offsets, nullptr, E);
+  constexpr int BM = 256, BN = 256;
+  GemmArgs a{};
+  a.offsets = offsets;
+  a.E = E;
   a.A = static_cast<const bf16_t*>(a_);
   a.B = static_cast<const bf16_t*>(b_);
   a.C = static_cast<bf16_t*>(c_out);
@@ -476,5 +926,5 @@ extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* o
   a.m_tiles = (M + BM - 1) / BM;
   a.n_tiles = (Nc + BN - 1) / BN;
   a.total_tiles = static_cast<int64_t>(E) * a.m_tiles * a.n_tiles;
-  return launch<false, false, 1, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_wgrad");
+  return launch<BM, BN, false, false, 1, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_wgrad");
 }

@@ -64,7 +64,7 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
     st = L.stream_ptr(dev)
     L.call("ffmoe_route_fwd", L.ptr(x), L.ptr(gate), None, L.ptr(bias), N, D, E, k, gating,
            int(need_ssum), L.ptr(logits), L.ptr(topk_idx), L.ptr(topk_w), L.ptr(lse), L.ptr(ws), st)
-    L.call("ffmoe_route_scan", N, E, k, mt, L.gemm_tile_rows(), aux_coeff, z_coeff, gating,
+    L.call("ffmoe_route_scan", N, E, k, mt, L.gemm_tile_rows(N * k, E), aux_coeff, z_coeff, gating,
            L.ptr(ws), L.ptr(counts), L.ptr(offsets), L.ptr(tile_offsets), L.ptr(stats),
            L.ptr(istats), st)
     return [logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats, ws]
@@ -93,10 +93,11 @@ def _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, save_up, st):
     up = torch.empty(T, H2, dtype=_BF16, device=dev) if save_up else None
     act = torch.empty(T, H, dtype=_BF16, device=dev)
     down = torch.empty(T, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_up_glu", L.ptr(xs), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), E, T,
-           D, H, activation, L.ptr(up), L.ptr(act), st)
-    L.call("ffmoe_gemm_down", L.ptr(act), L.ptr(w_down), L.ptr(offsets), L.ptr(tile_offsets), E, T,
-           H, D, L.ptr(down), st)
+    tr = L.gemm_tile_rows(T, E)
+    L.call("ffmoe_gemm_up_glu", L.ptr(xs), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
+           T, D, H, activation, L.ptr(up), L.ptr(act), st)
+    L.call("ffmoe_gemm_down", L.ptr(act), L.ptr(w_down), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
+           T, H, D, L.ptr(down), st)
     return up, act, down
 
 
@@ -177,11 +178,12 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
            aux_coeff, z_coeff, N, D, E, k, gating, int(capacity_mode), L.ptr(wgo), L.ptr(gl),
            None, st)
     gup = torch.empty(T, H2, dtype=_BF16, device=dev)
+    tr = L.gemm_tile_rows(T, E)
     L.call("ffmoe_gemm_dgrad_glu", L.ptr(wgo), L.ptr(w_down), L.ptr(up), L.ptr(offsets),
-           L.ptr(tile_offsets), E, T, D, H, activation, L.ptr(gup), st)
+           L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(gup), st)
     ghb = torch.empty(T, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_dgrad", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), E, T,
-           H, D, L.ptr(ghb), st)
+    L.call("ffmoe_gemm_dgrad", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
+           T, H, D, L.ptr(ghb), st)
     # the two small dense gate products are plain library GEMMs (hipBLASLt)
     addend = torch.matmul(gl, gate)
     dx = torch.empty(N, D, dtype=_BF16, device=dev)

@@ -134,8 +134,16 @@ int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
 /* ------------------------------------------------------------------------ */
 /* Expert grouped GEMMs (bf16 MFMA, fp32 accumulate, bf16 out).             */
 /* Row groups come from offsets[E+1] and tile_offsets[E+1] on the device;   */
-/* max_rows is the host-side upper bound of offsets[E] (N*k).               */
+/* tile_offsets must have been computed (ffmoe_route_scan's gemm_bm) for    */
+/* the same tile_rows; max_rows is the host-side upper bound of offsets[E]  */
+/* (N*k).                                                                   */
 /* ------------------------------------------------------------------------ */
+
+/* Row-tile height the grouped GEMMs use for max_rows rows over E experts
+ * (128 or 256).  Pass it as `gemm_bm` to ffmoe_route_scan and as `tile_rows`
+ * to the grouped GEMMs.  No reference counterpart (the reference pads every
+ * expert to max_tokens rows). */
+int ffmoe_gemm_tile_rows(int64_t max_rows, int E);
 
 /* up = x_sorted · w_up[e]^T and the fused GLU:
  *   up_out [rows, 2H] (pre-activation, may be NULL), act_out [rows, H].
@@ -143,33 +151,28 @@ int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
  *   (activations.py:27-74, :145-186).  w_up [E, 2H, D]: rows [0,H) gate half,
  *   [H,2H) up half. */
 int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up,
-                      const int32_t* offsets, const int32_t* tile_offsets, int E,
-                      int64_t max_rows, int D, int H, int activation,
-                      void* up_out, void* act_out, void* stream);
+                      const int32_t* offsets, const int32_t* tile_offsets,
+                      int tile_rows, int E, int64_t max_rows, int D, int H,
+                      int activation, void* up_out, void* act_out, void* stream);
 
 /* down [rows, D] = act · w_down[e]^T.  w_down [E, D, H].
  * Replaces: down bmm (fused_moe.py:441). */
 int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
-                    const int32_t* tile_offsets, int E, int64_t max_rows, int H,
-                    int D, void* down_out, void* stream);
+                    const int32_t* tile_offsets, int tile_rows, int E,
+                    int64_t max_rows, int H, int D, void* down_out, void* stream);
 
 /* gup [rows, 2H] = GLU_backward(wgo · w_down[e], up).
  * Replaces: dX-down bmm (fused_moe.py:547) + `activation_backward`
  *   (activations.py:77-142, :189-231). */
 int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,
                          const int32_t* offsets, const int32_t* tile_offsets,
-                         int E, int64_t max_rows, int D, int H, int activation,
-                         void* gup_out, void* stream);
+                         int tile_rows, int E, int64_t max_rows, int D, int H,
+                         int activation, void* gup_out, void* stream);
 
 /* ghb [rows, D] = gup · w_up[e].  Replaces: dX-up bmm (fused_moe.py:553). */
 int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t* offsets,
-                     const int32_t* tile_offsets, int E, int64_t max_rows, int H,
-                     int D, void* ghb_out, void* stream);
-
-/* Row-tile height (BM) of the grouped GEMMs: pass it as `gemm_bm` to
- * ffmoe_route_scan so tile_offsets match the GEMM kernels.  No reference
- * counterpart (the reference pads every expert to max_tokens rows). */
-int ffmoe_gemm_tile_rows(void);
+                     const int32_t* tile_offsets, int tile_rows, int E,
+                     int64_t max_rows, int H, int D, void* ghb_out, void* stream);
 
 /* Selects how MN-contiguous GEMM operands are read from LDS: 1 (default) =
  * ds_read_b64_tr_b16 transpose reads, 0 = element-wise reads.  Returns the

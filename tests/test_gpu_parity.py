@@ -104,7 +104,8 @@ def test_permutation_bit_exact(N, E, k, mt, cap):
     own = exp_rows >= 0
     j = np.nonzero(own)[0]
     assert torch.equal(xs.cpu()[exp_rows[own]], x[j // k])
-    bm = __import__("flashfusedmoe_amd._lib", fromlist=["x"]).gemm_tile_rows()
+    from flashfusedmoe_amd import _lib as L
+    bm = L.gemm_tile_rows(N * k, E)
     tiles = -(-np.minimum(exp_counts, mt) // bm)
     assert np.array_equal(tile_off.cpu().numpy()[1:], np.cumsum(tiles))
 
@@ -132,10 +133,10 @@ def test_grouped_gemms_against_fp32(sizes, D, H, tr, _lib):
     L = _lib
     E = len(sizes)
     xs, wu, wd, off = _groups(E, sizes, D, H, seed=sum(sizes) + D)
-    bm = L.gemm_tile_rows()
+    T = xs.shape[0]
+    bm = L.gemm_tile_rows(T, E)
     tiles = np.zeros(E + 1, dtype=np.int32)
     tiles[1:] = np.cumsum([-(-s // bm) for s in sizes])
-    T = xs.shape[0]
     dev = "cuda"
     xs_g, wu_g, wd_g = cuda(xs, wu, wd)
     off_g = torch.from_numpy(off).to(dev)
@@ -146,17 +147,17 @@ def test_grouped_gemms_against_fp32(sizes, D, H, tr, _lib):
     act = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     down = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
     L.call("ffmoe_gemm_up_glu", xs_g.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
-           E, T, D, H, 0, up.data_ptr(), act.data_ptr(), st)
+           bm, E, T, D, H, 0, up.data_ptr(), act.data_ptr(), st)
     L.call("ffmoe_gemm_down", act.data_ptr(), wd_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
-           E, T, H, D, down.data_ptr(), st)
+           bm, E, T, H, D, down.data_ptr(), st)
     g = torch.Generator().manual_seed(5)
     wgo = torch.randn(T, D, generator=g).to(torch.bfloat16).cuda()
     gup = torch.empty(T, 2 * H, dtype=torch.bfloat16, device=dev)
     L.call("ffmoe_gemm_dgrad_glu", wgo.data_ptr(), wd_g.data_ptr(), up.data_ptr(), off_g.data_ptr(),
-           til_g.data_ptr(), E, T, D, H, 0, gup.data_ptr(), st)
+           til_g.data_ptr(), bm, E, T, D, H, 0, gup.data_ptr(), st)
     ghb = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
     L.call("ffmoe_gemm_dgrad", gup.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
-           E, T, H, D, ghb.data_ptr(), st)
+           bm, E, T, H, D, ghb.data_ptr(), st)
     dwd = torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
     L.call("ffmoe_gemm_wgrad", wgo.data_ptr(), act.data_ptr(), off_g.data_ptr(), E, D, H,
            dwd.data_ptr(), st)
