@@ -67,15 +67,22 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Logistic sigmoid from the hardware exp2 and reciprocal (v_exp_f32,
+// v_rcp_f32: about 1 ulp each in fp32, far below the bf16 rounding every GLU
+// result goes through).  Saturates cleanly: 1/(1 + inf) = 0.
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
 // GLU activations in fp32 (the reference computes them in fp32 from bf16
 // operands, activations.py:27-142).  tanh is taken as 2*sigmoid(2z) - 1
 // (activations.py:21-24).
 __device__ __forceinline__ float glu_fwd(int act, float g, float u) {
   if (act == FFMOE_ACT_SWIGLU) {
-    return g * (1.0f / (1.0f + expf(-g))) * u;
+    return g * fast_sigmoid(g) * u;
   } else if (act == FFMOE_ACT_GEGLU) {
     const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
-    const float th = 2.0f / (1.0f + expf(-2.0f * inner)) - 1.0f;
+    const float th = 2.0f * fast_sigmoid(2.0f * inner) - 1.0f;
     return 0.5f * g * (1.0f + th) * u;
   } else {
     const float r = g > 0.0f ? g : 0.0f;
@@ -87,12 +94,12 @@ __device__ __forceinline__ float glu_fwd(int act, float g, float u) {
 __device__ __forceinline__ void glu_bwd(int act, float ga, float g, float u, float* gg,
                                         float* gu) {
   if (act == FFMOE_ACT_SWIGLU) {
-    const float s = 1.0f / (1.0f + expf(-g));
+    const float s = fast_sigmoid(g);
     *gu = ga * g * s;
     *gg = ga * u * (s * (1.0f + g * (1.0f - s)));
   } else if (act == FFMOE_ACT_GEGLU) {
     const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
-    const float th = 2.0f / (1.0f + expf(-2.0f * inner)) - 1.0f;
+    const float th = 2.0f * fast_sigmoid(2.0f * inner) - 1.0f;
     const float gelu = 0.5f * g * (1.0f + th);
     const float dinner = 0.7978845608028654f * (1.0f + 3.0f * 0.044715f * g * g);
     const float dgelu = 0.5f * (1.0f + th) + 0.5f * g * (1.0f - th * th) * dinner;
