@@ -173,7 +173,7 @@ def main():
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-tokens", type=int, default=2048)
+    ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--no-kernels", action="store_true", help="skip per-kernel timing")
     args = ap.parse_args()
     if args.gpus != 1:
