@@ -114,8 +114,7 @@ __device__ __forceinline__ bf16x8_t lds_frag_mn(const bf16_t* t, int c0, int ks,
 }
 
 __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
-  return make_uint2(static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16),
-                    static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16));
+  return make_uint2(pack_bf16x2(a, b), pack_bf16x2(c, d));
 }
 
 __device__ __forceinline__ void unpack4(uint2 v, float* f) {
@@ -460,22 +459,25 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Direct-to-LDS pipeline (the main path): BK = 32, a ring of kStages LDS
-// stages filled by buffer_load_dwordx4 ... lds (each wave instruction writes
-// 1 KiB of consecutive LDS; per-lane source addresses implement the swizzle;
+// Direct-to-LDS pipeline (the main path): BK = 64, two LDS stages filled by
+// buffer_load_dwordx4 ... lds (each wave instruction writes 1 KiB of
+// consecutive LDS; per-lane source addresses implement the swizzle;
 // out-of-range rows read as zero through the buffer descriptor's bounds).
-//   K-contiguous stage tile [R][32]: 16-byte chunk c of row r stored at
-//     chunk c ^ ((r >> 2) & 3): the 16 rows one ds_read_b128 cycle serves hit
+// Every row segment a stage loads is a whole 128-byte line (64 bf16 of a
+// K-contiguous row, or 256+ bf16 of an MN-contiguous k-row): half-line
+// segments halve what the L2 delivers to a CU.
+//   K-contiguous stage tile [R][64]: 16-byte chunk c of row r stored at
+//     chunk c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128 cycle serves hit
 //     16 distinct 16-byte bank slots (64 banks x 4 bytes).
-//   MN-contiguous stage tile [32][R]: chunk c of k-row k stored at
+//   MN-contiguous stage tile [64][R]: chunk c of k-row k stored at
 //     c ^ ((k & 3) << 2): the 2 x 4 rows x 32 bytes of one transpose-read
 //     cycle hit distinct bank slots.
-// Each K step: wait for this stage's loads (s_waitcnt vmcnt), one s_barrier,
-// issue the loads of the stage kStages-1 ahead into the buffer freed by the
-// previous step, then the MFMAs.
-// ---------------------------------------------------------------------------
-constexpr int DL_BK = 32;
-constexpr int kStages = 4;
+// Each 64-K stage is four MFMA k-steps of 16; operand fragments are
+// double-buffered in registers.  Before the last k-step of stage kt: wait for
+// stage kt+1's loads, one s_barrier, refill stage kt's buffer with stage
+// kt+2, read stage kt+1's first fragments, then run the last k-step.
+constexpr int DL_BK = 64;
+constexpr int kStages = 2;
 
 __device__ __forceinline__ void wait_vmcnt_le(int n) {
   // s_waitcnt with only the vector-memory count constrained (expcnt and
@@ -508,7 +510,8 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int A_EL = BM * DL_BK, B_EL = BN * DL_BK;  // elements per stage tile
   constexpr int STAGE = A_EL + B_EL;
-  constexpr int LA = BM / 64, LB = BN / 64;  // 16-byte loads per thread per stage
+  constexpr int LA = BM * DL_BK / 8 / kThreads;  // 16-byte loads per thread per stage
+  constexpr int LB = BN * DL_BK / 8 / kThreads;
   constexpr int LDC = BN + 8;                // C staging row stride
   constexpr int SMEM = (kStages * STAGE > BM * LDC) ? kStages * STAGE : BM * LDC;
   static_assert(EPI != EPI_GLU_FWD || (TN % 2 == 0), "GLU forward pairs gate/up tiles");
@@ -571,7 +574,7 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   for (int i = 0; i < LA; ++i) {
     const int pos = i * kThreads + tid;
     if constexpr (A_KC) {
-      const int r = pos >> 2, c = (pos & 3) ^ ((r >> 2) & 3);
+      const int r = pos >> 3, c = (pos & 7) ^ ((r >> 1) & 7);
       offa[i] = static_cast<uint32_t>((r * p.lda + c * 8) * 2);
     } else {
       const int k = pos / (BM / 8), c = (pos % (BM / 8)) ^ ((k & 3) << 2);
@@ -582,7 +585,7 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   for (int i = 0; i < LB; ++i) {
     const int pos = i * kThreads + tid;
     if constexpr (B_KC) {
-      const int r = pos >> 2, c = (pos & 3) ^ ((r >> 2) & 3);
+      const int r = pos >> 3, c = (pos & 7) ^ ((r >> 1) & 7);
       int brow;
       if constexpr (EPI == EPI_GLU_FWD) {
         const int a = a0 + (r % (BN / 2));
@@ -635,11 +638,11 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  static_assert(DL_BK == 32, "two MFMA k-steps per stage");
+  static_assert(DL_BK == 64 && kStages == 2, "four MFMA k-steps per stage, two stages");
   // MFMA operand fragments of one k-step (16 of K), double-buffered in
-  // registers: set 0 holds k-step 0 of a stage, set 1 k-step 1.  The reads of
-  // one set overlap the MFMAs of the other; k-step 0 of stage kt+1 is read
-  // right after the barrier that publishes it, during k-step 1's MFMAs.
+  // registers (sets F0 / F1): the reads of one set overlap the MFMAs of the
+  // other.  k-step 0 of stage kt+1 is read right after the barrier that
+  // publishes it, during k-step 3 of stage kt.
   bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
   auto read_ks = [&](int buf, int ks, bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) {
     const bf16_t* at = smem + buf * STAGE;
@@ -649,7 +652,7 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
       const int r0 = wm * WM + tm * 32;
       if constexpr (A_KC) {
         const int r = r0 + (lane & 31);
-        const int c = (ks * 2 + (lane >> 5)) ^ ((r >> 2) & 3);
+        const int c = (ks * 2 + (lane >> 5)) ^ ((r >> 1) & 7);
         fa[tm] = *reinterpret_cast<const bf16x8_t*>(at + r * DL_BK + c * 8);
       } else {
         fa[tm] = lds_frag_mn_sw<BM>(at, r0, ks, lane);
@@ -660,7 +663,7 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
       const int c0 = tile_col(tn);
       if constexpr (B_KC) {
         const int r = c0 + (lane & 31);
-        const int c = (ks * 2 + (lane >> 5)) ^ ((r >> 2) & 3);
+        const int c = (ks * 2 + (lane >> 5)) ^ ((r >> 1) & 7);
         fb[tn] = *reinterpret_cast<const bf16x8_t*>(bt + r * DL_BK + c * 8);
       } else {
         fb[tn] = lds_frag_mn_sw<BN>(bt, c0, ks, lane);
@@ -677,13 +680,12 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   // LDS fragment reads per k-step (a transpose-read fragment takes two)
   constexpr int NR = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);
   constexpr int NM = TM * TN;  // MFMAs per k-step
-  // Stages in flight: before the barrier of step kt, steps up to kt+kStages-1
-  // have been issued and step kt+1 must have landed, so kStages-2 steps of
-  // loads may stay outstanding: s_waitcnt vmcnt(that) and lgkmcnt(0).
-  constexpr int kInFlight = (kStages - 2) * (LA + LB);
-  constexpr int kWaitLoads = (kInFlight & 15) | ((kInFlight >> 4) << 14) | 0x70 | 0xF00;
-  constexpr int kWaitLoadsLds = (kInFlight & 15) | ((kInFlight >> 4) << 14) | 0x70;
-  static_assert(kInFlight < 64, "vmcnt range");
+  constexpr int kLoads = LA + LB;  // loads per thread per stage
+  static_assert(kLoads < 64, "vmcnt range");
+  // prologue: stage 0 landed (stage 1 may be in flight), LDS count free
+  constexpr int kWaitStage0 = (kLoads & 15) | ((kLoads >> 4) << 14) | 0x70 | 0xF00;
+  // in the loop: stage kt+1 landed and this wave's LDS reads retired
+  constexpr int kWaitAll = 0x0070;
 
   // Scheduling of one k-step region: pair each LDS read and each stage load
   // with an MFMA, so one wave per SIMD issues them in the MFMAs' shadow.
@@ -697,31 +699,42 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   };
 
   if (nk > 0) {
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue(s, s);
-    __builtin_amdgcn_s_waitcnt(kWaitLoads);  // stage 0 landed
+    issue(0, 0);
+    issue(1, 1);
+    __builtin_amdgcn_s_waitcnt(kWaitStage0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    issue(kStages - 1, kStages - 1);
     read_ks(0, 0, fa0, fb0);
     for (int kt = 0; kt + 1 < nk; ++kt) {
-      // k-step 1 of stage kt: fragments read while k-step 0 runs
-      read_ks(kt & (kStages - 1), 1, fa1, fb1);
+      const int cur = kt & 1;
+      read_ks(cur, 1, fa1, fb1);
       mfma_ks(fa0, fb0);
       interleave(0);
-      // publish stage kt+1 (and retire this wave's reads of stage kt)
-      __builtin_amdgcn_s_waitcnt(kWaitLoadsLds);
+      read_ks(cur, 2, fa0, fb0);
+      mfma_ks(fa1, fb1);
+      interleave(0);
+      read_ks(cur, 3, fa1, fb1);
+      mfma_ks(fa0, fb0);
+      interleave(0);
+      // publish stage kt+1; every wave's reads of stage kt have retired
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      // refill stage kt's buffer, read k-step 0 of stage kt+1, run k-step 1
-      issue(kt + kStages, kt & (kStages - 1));
-      read_ks((kt + 1) & (kStages - 1), 0, fa0, fb0);
+      // refill stage kt's buffer with stage kt+2, read k-step 0 of stage
+      // kt+1, run k-step 3 of stage kt
+      issue(kt + 2, cur);
+      read_ks(cur ^ 1, 0, fa0, fb0);
       mfma_ks(fa1, fb1);
-      interleave(LA + LB);
+      interleave(kLoads);
     }
-    read_ks((nk - 1) & (kStages - 1), 1, fa1, fb1);
+    const int last = (nk - 1) & 1;
+    read_ks(last, 1, fa1, fb1);
+    mfma_ks(fa0, fb0);
+    read_ks(last, 2, fa0, fb0);
+    mfma_ks(fa1, fb1);
+    read_ks(last, 3, fa1, fb1);
     mfma_ks(fa0, fb0);
     mfma_ks(fa1, fb1);
   }
