@@ -70,7 +70,7 @@ def kernel_rates(c, x, gate, wu, wd, go, reps=20):
     T = N * k
     mt = (N * k + E - 1) // E
     mt += max(mt, k)
-    (logits, idx, tw, lse, counts, off, til, stats, istats, ws) = ops.route(
+    (logits, idx, tw, lse, counts, off, til, stats, istats, ws, _aux, _z) = ops.route(
         x, gate, None, k, 0, mt, c["aux"], c["z"], False)
     out, tw2, row_of, xs, up, act, down = ops.experts_forward(
         x, wu, wd, idx, tw, counts, off, til, ws, k, 0, mt, False, True)
@@ -85,7 +85,9 @@ def kernel_rates(c, x, gate, wu, wd, go, reps=20):
     dwd = torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
     dwu = torch.empty(E, 2 * H, D, dtype=torch.bfloat16, device=dev)
     dx = torch.empty(N, D, dtype=torch.bfloat16, device=dev)
-    addend = torch.zeros(N, D, dtype=torch.bfloat16, device=dev)
+    gpart = torch.empty(int(L.load().ffmoe_gate_grad_workspace_bytes(N, D, E)), dtype=torch.uint8,
+                        device=dev)
+    dgate = torch.empty(E, D, dtype=torch.bfloat16, device=dev)
     xs2 = torch.empty_like(xs)
     row2 = torch.empty_like(row_of)
     tw3 = tw.clone()
@@ -94,15 +96,16 @@ def kernel_rates(c, x, gate, wu, wd, go, reps=20):
     dn_f = 2.0 * rows * H * D
     b = 2  # bytes per bf16
     tr = L.gemm_tile_rows(T, E)
+    gws = P(L.gemm_workspace(xs.device, st))
     launches = {
         "gemm_up_glu": (lambda: L.call("ffmoe_gemm_up_glu", P(xs), P(wu), P(off), P(til), tr, E, T, D,
-                                       H, 0, P(up), P(act), st), up_f, "flop"),
+                                       H, 0, P(up), P(act), gws, st), up_f, "flop"),
         "gemm_down": (lambda: L.call("ffmoe_gemm_down", P(act), P(wd), P(off), P(til), tr, E, T, H, D,
-                                     P(down), st), dn_f, "flop"),
+                                     P(down), gws, st), dn_f, "flop"),
         "gemm_dgrad_glu": (lambda: L.call("ffmoe_gemm_dgrad_glu", P(wgo), P(wd), P(up), P(off), P(til),
-                                          tr, E, T, D, H, 0, P(gup), st), dn_f, "flop"),
+                                          tr, E, T, D, H, 0, P(gup), gws, st), dn_f, "flop"),
         "gemm_dgrad": (lambda: L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), tr, E, T, H,
-                                      D, P(ghb), st), up_f, "flop"),
+                                      D, P(ghb), gws, st), up_f, "flop"),
         "gemm_wgrad_down": (lambda: L.call("ffmoe_gemm_wgrad", P(wgo), P(act), P(off), E, D, H, P(dwd),
                                            st), dn_f, "flop"),
         "gemm_wgrad_up": (lambda: L.call("ffmoe_gemm_wgrad", P(gup), P(xs), P(off), E, 2 * H, D, P(dwu),
@@ -120,8 +123,11 @@ def kernel_rates(c, x, gate, wu, wd, go, reps=20):
                                      P(logits), P(lse), P(counts), None, P(gz), c["aux"], c["z"], N, D,
                                      E, k, 0, 0, P(wgo), P(gl), None, st),
                       N * D * b + 2 * rows * D * b + N * E * 2 * b + N * k * 16, "byte"),
-        "dx_reduce": (lambda: L.call("ffmoe_combine", P(ghb), P(row_of), None, P(addend), N, D, k,
-                                     P(dx), st), rows * D * b + 2 * N * D * b + N * k * 4, "byte"),
+        "dx_reduce": (lambda: L.call("ffmoe_dx_reduce", P(ghb), P(row_of), P(gl), P(gate), N, D, E, k,
+                                     P(dx), st),
+                      rows * D * b + N * D * b + N * E * b + E * D * b + N * k * 4, "byte"),
+        "gate_grad": (lambda: L.call("ffmoe_gate_grad", P(gl), P(x), N, D, E, P(gpart), P(dgate), st),
+                      N * D * b + N * E * b + E * D * b, "byte"),
     }
     res = {}
     for name, (fn, work, kind) in launches.items():
@@ -175,6 +181,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--no-kernels", action="store_true", help="skip per-kernel timing")
+    ap.add_argument("--no-layer", action="store_true", help="skip the MoELayer (shared expert) timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -227,7 +234,7 @@ def main():
         out, losses = layer(xl)
         torch.autograd.backward([out, losses["z_loss"]], [go, one])
 
-    layer_ms = time_events(layer_step, max(5, args.steps // 2))
+    layer_ms = None if args.no_layer else time_events(layer_step, max(5, args.steps // 2))
 
     kernels = {} if args.no_kernels else kernel_rates(
         c, *(p.detach() for p in params), go)
@@ -260,8 +267,8 @@ def main():
                                "aux0.01 z1e-3 allow_dropped_tokens=True",
                    "global_batch": c["N"], "parallelism": "none (1 GPU)"},
         "expert_gemm_mfma_frac_of_step": round(step_mfma_frac, 4),
-        "moelayer_shared_expert": {"ms_per_step": round(layer_ms, 4),
-                                   "tokens_per_s": round(c["N"] / (layer_ms * 1e-3), 1)},
+        "moelayer_shared_expert": None if layer_ms is None else {
+            "ms_per_step": round(layer_ms, 4), "tokens_per_s": round(c["N"] / (layer_ms * 1e-3), 1)},
         "roofline": roofline,
         "kernels": {n: {"ms": round(v["ms"], 5), "rate": round(v["rate"], 2), "unit": v["unit"],
                         "frac": round(v["frac"], 4)} for n, v in kernels.items()},

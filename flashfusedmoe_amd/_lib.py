@@ -20,6 +20,7 @@ GATING = {"softmax": 0, "sigmoid": 1}
 ACTIVATION = {"swiglu": 0, "geglu": 1, "relu_squared": 2}
 MAX_EXPERTS = 256
 MAX_TOPK = 16
+MAX_FUSED_GATE_E = 32
 STAT_AUX, STAT_Z, STAT_IMBALANCE, STAT_DROP_FRAC, NUM_STATS = 0, 1, 2, 3, 4
 ISTAT_MAX, ISTAT_MIN, ISTAT_DROPPED, NUM_ISTATS = 0, 1, 2, 4
 
@@ -34,16 +35,20 @@ SIGNATURES = {
     "ffmoe_version": (_I, []),
     "ffmoe_route_workspace_bytes": (ctypes.c_size_t, [_L, _I, _I]),
     "ffmoe_route_fwd": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
-    "ffmoe_route_scan": (_I, [_L, _I, _I, _I, _I, _F, _F, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "ffmoe_route_scan": (_I, [_L, _I, _I, _I, _I, _F, _F, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "ffmoe_permute": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "ffmoe_gemm_tile_rows": (_I, [_L, _I]),
     "ffmoe_set_lds_transpose": (_I, [_I]),
-    "ffmoe_gemm_up_glu": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
-    "ffmoe_gemm_down": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P]),
-    "ffmoe_gemm_dgrad_glu": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P]),
-    "ffmoe_gemm_dgrad": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P]),
+    "ffmoe_gemm_workspace_bytes": (_L, []),
+    "ffmoe_gemm_up_glu": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P, _P]),
+    "ffmoe_gemm_down": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P]),
+    "ffmoe_gemm_dgrad_glu": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
+    "ffmoe_gemm_dgrad": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P]),
     "ffmoe_gemm_wgrad": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
     "ffmoe_combine": (_I, [_P, _P, _P, _P, _L, _I, _I, _P, _P]),
+    "ffmoe_dx_reduce": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _P, _P]),
+    "ffmoe_gate_grad_workspace_bytes": (_L, [_L, _I, _I]),
+    "ffmoe_gate_grad": (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
     "ffmoe_route_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I,
                              _I, _I, _P, _P, _P, _P]),
     "ffmoe_glu_fwd": (_I, [_P, _L, _I, _I, _P, _P]),
@@ -105,6 +110,26 @@ def call(name, *args):
 def gemm_tile_rows(max_rows, E):
     """Row-tile height the grouped GEMMs use for max_rows rows over E experts."""
     return load().ffmoe_gemm_tile_rows(max_rows, E)
+
+
+_GEMM_WS = {}
+
+
+def gemm_workspace(device, stream):
+    """The grouped GEMMs' persistent-schedule workspace for (device, stream):
+    allocated zeroed once (its flags must start at zero; every GEMM call
+    leaves them zero), reused by every later call on that stream."""
+    import torch
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _GEMM_WS.get(key)
+    if ws is None:
+        with torch.cuda.device(key[0]):
+            nbytes = int(load().ffmoe_gemm_workspace_bytes())
+        if nbytes <= 0:
+            raise FFMoEError("ffmoe_gemm_workspace_bytes failed: no device")
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _GEMM_WS[key] = ws
+    return ws
 
 
 def route_workspace_bytes(N, E, k):

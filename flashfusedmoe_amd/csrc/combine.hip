@@ -45,6 +45,163 @@ __global__ __launch_bounds__(256) void combine_kernel(const bf16_t* __restrict__
   }
 }
 
+// dX reduce with the gate-gradient term fused (E <= FFMOE_MAX_FUSED_GATE_E):
+//   out[n] = bf16(bf16(sum_s ghb[src(row_of[n*k+s])]) + bf16(gl[n,:] . gate))
+// The sum over slots is fp32 in slot order (moe_ops.py:156-241 with unit
+// weights, fused_moe.py:556-561); the gl . gate product is fp32 over experts
+// in index order, rounded to bf16 as the reference's bf16 `gl @ gate` GEMM
+// output is (fused_moe.py:590).
+__global__ __launch_bounds__(256) void dx_reduce_kernel(const bf16_t* __restrict__ rows,
+                                                        const int32_t* __restrict__ row_of,
+                                                        const bf16_t* __restrict__ gl,
+                                                        const bf16_t* __restrict__ gate, int64_t N,
+                                                        int D, int E, int k,
+                                                        bf16_t* __restrict__ out) {
+  const int nvec = D / 8;
+  const int64_t total = N * nvec;
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
+       u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t n = u / nvec;
+    const int v = static_cast<int>(u % nvec);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < k; ++s) {
+      const int r = src_row(row_of[n * k + s]);
+      if (r < 0) continue;
+      float f[8];
+      unpack8(reinterpret_cast<const uint4*>(rows + static_cast<int64_t>(r) * D)[v], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += f[i];
+    }
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < E; ++e) {
+      const float g = bf16_to_f32(gl[n * E + e]);
+      float w[8];
+      unpack8(reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(e) * D)[v], w);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] += g * w[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = round_bf16(acc[i]) + round_bf16(a[i]);
+    reinterpret_cast<uint4*>(out + n * D)[v] = pack8(acc);
+  }
+}
+
+// Gate weight gradient dgate[E, D] = gl^T x (fused_moe.py:591), E <=
+// FFMOE_MAX_FUSED_GATE_E.  Pass 1: a block takes a 256-column slice of
+// kGateChunk tokens; its gl rows are staged in LDS, each of the 4 waves
+// accumulates a quarter of the tokens in token order (lane l owns 4 columns,
+// all of a wave's x loads in flight together), and the 4 wave partials are
+// added in wave order through LDS into one fp32 partial per block.  Pass 2
+// sums the partials in chunk order and rounds to bf16.  x is read once;
+// deterministic.
+constexpr int kGateChunk = 64;
+constexpr int kGateWaves = 4;
+constexpr int kGateBatch = kGateChunk / kGateWaves;
+
+template <int EMAX>
+__global__ __launch_bounds__(256) void gate_grad_partial_kernel(const bf16_t* __restrict__ gl,
+                                                                const bf16_t* __restrict__ x,
+                                                                int64_t N, int D, int E,
+                                                                float* __restrict__ part) {
+  __shared__ float s_gl[kGateChunk * EMAX];
+  __shared__ float4 s_red[kGateWaves][8][64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c0 = blockIdx.x * 256 + lane * 4;
+  const int64_t chunk = blockIdx.y;
+  const int64_t n0 = chunk * kGateChunk;
+  const int nt = static_cast<int>(min<int64_t>(kGateChunk, N - n0));
+  for (int i = tid; i < kGateChunk * E; i += 256)
+    s_gl[i] = i < nt * E ? bf16_to_f32(gl[n0 * E + i]) : 0.0f;
+  __syncthreads();
+  float acc[EMAX][4];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[e][i] = 0.0f;
+  const bool col_ok = c0 < D;
+  const int t0 = wave * kGateBatch;
+  uint2 xv[kGateBatch];
+#pragma unroll
+  for (int j = 0; j < kGateBatch; ++j) {
+    const int t = t0 + j;
+    xv[j] = (col_ok && t < nt) ? *reinterpret_cast<const uint2*>(x + (n0 + t) * D + c0)
+                               : make_uint2(0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < kGateBatch; ++j) {
+    const int t = t0 + j;
+    float xf[4];
+    xf[0] = __uint_as_float(xv[j].x << 16);
+    xf[1] = __uint_as_float(xv[j].x & 0xffff0000u);
+    xf[2] = __uint_as_float(xv[j].y << 16);
+    xf[3] = __uint_as_float(xv[j].y & 0xffff0000u);
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) {
+      if (e < E) {
+        const float g = s_gl[t * E + e];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[e][i] += g * xf[i];
+      }
+    }
+  }
+  // wave partials -> one block partial, 8 experts at a time, waves in order
+#pragma unroll
+  for (int eb = 0; eb < EMAX; eb += 8) {
+    if (eb >= E) break;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      s_red[wave][j][lane] = make_float4(acc[eb + j][0], acc[eb + j][1], acc[eb + j][2], acc[eb + j][3]);
+    __syncthreads();
+    // thread (wave w, lane l) finishes experts eb + 2w, eb + 2w + 1 of lane l's columns
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * wave + h;
+      const int e = eb + j;
+      float4 r = s_red[0][j][lane];
+#pragma unroll
+      for (int w = 1; w < kGateWaves; ++w) {
+        const float4 v = s_red[w][j][lane];
+        r.x += v.x;
+        r.y += v.y;
+        r.z += v.z;
+        r.w += v.w;
+      }
+      if (col_ok && e < E)
+        *reinterpret_cast<float4*>(part + (chunk * E + e) * static_cast<int64_t>(D) + c0) = r;
+    }
+    __syncthreads();
+  }
+}
+
+// 64 outputs per block, 4 threads per output: thread q sums parts q, q+4, ...
+// in order, then thread 0 of each output adds the four in order.
+__global__ __launch_bounds__(256) void gate_grad_final_kernel(const float* __restrict__ part,
+                                                              int64_t nparts, int D, int E,
+                                                              bf16_t* __restrict__ out) {
+  __shared__ float s[256];
+  const int tid = threadIdx.x;
+  const int q = tid >> 6;
+  const int64_t total = static_cast<int64_t>(E) * D;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 64 + (tid & 63);
+  float acc = 0.0f;
+  if (i < total) {
+    int64_t c = q;
+    for (; c + 12 < nparts; c += 16) {
+      const float a0 = part[c * total + i], a1 = part[(c + 4) * total + i];
+      const float a2 = part[(c + 8) * total + i], a3 = part[(c + 12) * total + i];
+      acc += a0;
+      acc += a1;
+      acc += a2;
+      acc += a3;
+    }
+    for (; c < nparts; c += 4) acc += part[c * total + i];
+  }
+  s[tid] = acc;
+  __syncthreads();
+  if (q == 0 && i < total) out[i] = f32_to_bf16(((s[tid] + s[tid + 64]) + s[tid + 128]) + s[tid + 192]);
+}
+
 // Routing backward, one wave per token n:
 //   g_w[s] = <down[src_s], go[n]> (fp32)                 fused_moe.py:527-535
 //   wgo[row_s] = bf16(go[n] * bf16(w_s)) for owned rows   moe_ops.py:248-288
@@ -237,6 +394,51 @@ extern "C" int ffmoe_combine(const void* rows, const int32_t* row_of, const floa
                      static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(rows), row_of,
                      topk_w, static_cast<const bf16_t*>(addend), N, D, k, static_cast<bf16_t*>(out));
   if (check_launch("combine_kernel")) return 1;
+  return clear_error();
+}
+
+extern "C" int ffmoe_dx_reduce(const void* ghb, const int32_t* row_of, const void* gl,
+                               const void* gate, int64_t N, int D, int E, int k, void* out,
+                               void* stream) {
+  if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_dx_reduce: D must be a positive multiple of 8");
+  if (k < 1 || k > FFMOE_MAX_TOPK) return set_error("ffmoe_dx_reduce: bad k");
+  if (E < 1 || E > FFMOE_MAX_FUSED_GATE_E) return set_error("ffmoe_dx_reduce: E out of range");
+  hipLaunchKernelGGL(dx_reduce_kernel, dim3(grid_for(N * (D / 8))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(ghb), row_of,
+                     static_cast<const bf16_t*>(gl), static_cast<const bf16_t*>(gate), N, D, E, k,
+                     static_cast<bf16_t*>(out));
+  if (check_launch("dx_reduce_kernel")) return 1;
+  return clear_error();
+}
+
+extern "C" int64_t ffmoe_gate_grad_workspace_bytes(int64_t N, int D, int E) {
+  if (N <= 0 || D <= 0 || E <= 0) return 0;
+  return ((N + kGateChunk - 1) / kGateChunk) * static_cast<int64_t>(E) * D * 4;
+}
+
+extern "C" int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, int E,
+                               void* workspace, void* dgate, void* stream) {
+  if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_gate_grad: D must be a positive multiple of 8");
+  if (E < 1 || E > FFMOE_MAX_FUSED_GATE_E) return set_error("ffmoe_gate_grad: E out of range");
+  const int64_t nchunk = (N + kGateChunk - 1) / kGateChunk;
+  if (nchunk > 65535) return set_error("ffmoe_gate_grad: N too large (at most 4194240 tokens)");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  const dim3 grid(static_cast<unsigned>((D + 255) / 256), static_cast<unsigned>(nchunk));
+  if (E <= 8)
+    hipLaunchKernelGGL(gate_grad_partial_kernel<8>, grid, dim3(256), 0, st,
+                       static_cast<const bf16_t*>(gl), static_cast<const bf16_t*>(x), N, D, E, part);
+  else if (E <= 16)
+    hipLaunchKernelGGL(gate_grad_partial_kernel<16>, grid, dim3(256), 0, st,
+                       static_cast<const bf16_t*>(gl), static_cast<const bf16_t*>(x), N, D, E, part);
+  else
+    hipLaunchKernelGGL(gate_grad_partial_kernel<32>, grid, dim3(256), 0, st,
+                       static_cast<const bf16_t*>(gl), static_cast<const bf16_t*>(x), N, D, E, part);
+  if (check_launch("gate_grad_partial_kernel")) return 1;
+  const int64_t total = static_cast<int64_t>(E) * D;
+  hipLaunchKernelGGL(gate_grad_final_kernel, dim3(static_cast<unsigned>((total + 63) / 64)),
+                     dim3(256), 0, st, part, nchunk, D, E, static_cast<bf16_t*>(dgate));
+  if (check_launch("gate_grad_final_kernel")) return 1;
   return clear_error();
 }
 

@@ -22,6 +22,7 @@
 // Two LDS stages; the next stage's global loads are issued before the current
 // stage's MFMAs and land in LDS after them (one barrier per BK step).
 #include <string>
+#include <type_traits>
 
 #include "common.h"
 
@@ -55,6 +56,8 @@ struct GemmArgs {
   bf16_t* C2;        // GLU forward: pre-activation out [rows, 2H] (optional)
   int H;
   int act;
+  float* part;  // persistent kernel: fp32 partial tiles, one slot per block
+  int* flags;   // persistent kernel: one flag per block + an error word
 };
 
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
@@ -496,16 +499,79 @@ __device__ __forceinline__ void wait_vmcnt_le(int n) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
                                            static_cast<int>(bytes), 0x00020000);
 }
 
-// The body is a __device__ function (the buffer-descriptor type exists only
-// in the device pass); gemm_dl_kernel below is the launchable wrapper.
+// Which part of a tile's K range a block computes.  ROLE_FULL: all of it,
+// then the epilogue.  ROLE_PART: the later part; the fp32 partial goes to the
+// block's workspace slot and its flag is raised.  ROLE_OWNER: the first part;
+// the owner adds the partner block's partial (owner + partner, the same sum
+// whichever finishes first) and runs the epilogue.
+enum Role { ROLE_FULL = 0, ROLE_OWNER = 1, ROLE_PART = 2 };
+
+struct TileCoord {
+  int e, m0, n0, row_begin, row_end;
+  bool valid;
+};
+
+// Row-group tables are read through the constant address space: they do not
+// change during a launch, so the loads are scalar (s_load) even after the
+// kernel's own stores, where the compiler could not otherwise prove that.
+typedef __attribute__((address_space(4))) const int32_t const_i32_t;
+__device__ __forceinline__ int ld_const(const int32_t* p, int i) {
+  return ((const const_i32_t*)p)[i];
+}
+
+// Grouped-rows tile t of a grid of m_count row tiles x n_tiles column tiles.
+template <int BM, int BN>
+__device__ __forceinline__ TileCoord decode_rows_tile(const GemmArgs& p, int64_t t, int m_count) {
+  TileCoord c{};
+  int mt, nt;
+  grouped_order(t, m_count, p.n_tiles, &mt, &nt);
+  c.n0 = nt * BN;
+  c.valid = mt < ld_const(p.tile_offsets, p.E);
+  if (!c.valid) return c;
+  int lo = 0, hi = p.E - 1;  // last e with tile_offsets[e] <= mt
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (ld_const(p.tile_offsets, mid) <= mt) lo = mid; else hi = mid - 1;
+  }
+  c.e = lo;
+  c.row_begin = ld_const(p.offsets, lo) + (mt - ld_const(p.tile_offsets, lo)) * BM;
+  c.row_end = ld_const(p.offsets, lo + 1);
+  return c;
+}
+
+// Grouped-K (wgrad) tile t: expert-major, then grouped over M x N tiles.
+template <int BM, int BN>
+__device__ __forceinline__ TileCoord decode_k_tile(const GemmArgs& p, int64_t t) {
+  TileCoord c{};
+  const int64_t per_e = static_cast<int64_t>(p.m_tiles) * p.n_tiles;
+  c.e = static_cast<int>(t / per_e);
+  int mt, nt;
+  grouped_order(t - static_cast<int64_t>(c.e) * per_e, p.m_tiles, p.n_tiles, &mt, &nt);
+  c.m0 = mt * BM;
+  c.n0 = nt * BN;
+  c.row_begin = ld_const(p.offsets, c.e);
+  c.row_end = ld_const(p.offsets, c.e + 1);
+  c.valid = true;
+  return c;
+}
+
+constexpr int kSpinLimit = 1 << 22;  // flag polls before a wait gives up
+// buffer-instruction cache policy: sc1, device scope (coherent across XCDs)
+constexpr int kDeviceScope = 16;
+
+// One tile (K steps [k0, k1); k1 < 0: to the end of K).  The body is a
+// __device__ function (the buffer-descriptor type exists only in the device
+// pass); the kernels below loop over tiles with it.
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
-__device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
+__device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord& tc, int k0, int k1,
+                                             int role, int slot, int partner) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int A_EL = BM * DL_BK, B_EL = BN * DL_BK;  // elements per stage tile
@@ -514,41 +580,25 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   constexpr int LB = BN * DL_BK / 8 / kThreads;
   constexpr int LDC = BN + 8;                // C staging row stride
   constexpr int SMEM = (kStages * STAGE > BM * LDC) ? kStages * STAGE : BM * LDC;
+  constexpr int NF = TM * TN * 4;            // fp32 partial: float4s per thread
   static_assert(EPI != EPI_GLU_FWD || (TN % 2 == 0), "GLU forward pairs gate/up tiles");
   __shared__ __attribute__((aligned(1024))) bf16_t smem[SMEM];
 
-  const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
-  if (tile >= p.total_tiles) return;
-
-  int e, m0 = 0, n0;
-  int row_begin = 0, row_end = 0;
-  if constexpr (MODE == 0) {
-    int mt, nt;
-    grouped_order(tile, p.m_tiles, p.n_tiles, &mt, &nt);
-    n0 = nt * BN;
-    if (mt >= p.tile_offsets[p.E]) return;
-    int lo = 0, hi = p.E - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (p.tile_offsets[mid] <= mt) lo = mid; else hi = mid - 1;
-    }
-    e = lo;
-    row_begin = p.offsets[e] + (mt - p.tile_offsets[e]) * BM;
-    row_end = p.offsets[e + 1];
-  } else {
-    const int64_t per_e = static_cast<int64_t>(p.m_tiles) * p.n_tiles;
-    e = static_cast<int>(tile / per_e);
-    int mt, nt;
-    grouped_order(tile - static_cast<int64_t>(e) * per_e, p.m_tiles, p.n_tiles, &mt, &nt);
-    m0 = mt * BM;
-    n0 = nt * BN;
-    row_begin = p.offsets[e];
-    row_end = p.offsets[e + 1];
-  }
+  // tile coordinates are block-uniform; readfirstlane keeps them (and the
+  // buffer descriptors built from them) in scalar registers even where the
+  // compiler cannot prove the loads they came from uniform
+  const int e = __builtin_amdgcn_readfirstlane(tc.e);
+  const int m0 = __builtin_amdgcn_readfirstlane(tc.m0);
+  const int n0 = __builtin_amdgcn_readfirstlane(tc.n0);
+  const int row_begin = __builtin_amdgcn_readfirstlane(tc.row_begin);
+  const int row_end = __builtin_amdgcn_readfirstlane(tc.row_end);
   const int K = (MODE == 0) ? p.K : (row_end - row_begin);
   const int a0 = (EPI == EPI_GLU_FWD) ? n0 / 2 : 0;
 
-  const int tid = threadIdx.x;
+  // per-thread addressing is recomputed for every tile: hoisted out of a
+  // persistent block's tile loop it would occupy registers the whole time
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wm = wave >> 1, wn = wave & 1;
@@ -603,14 +653,14 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   const uint32_t stepa = A_KC ? DL_BK * 2 : static_cast<uint32_t>(DL_BK * p.lda * 2);
   const uint32_t stepb = B_KC ? DL_BK * 2 : static_cast<uint32_t>(DL_BK * p.ldb * 2);
 
-  const int nk = (K + DL_BK - 1) / DL_BK;
-  // Loads of K step `kstep` into stage buffer `buf`.  Steps past the end are
-  // still issued, with an out-of-range offset (the buffer returns zeros and
-  // moves no memory), so every step has the same number of loads in flight.
+  if (k1 < 0) k1 = (K + DL_BK - 1) / DL_BK;
+  // Loads of K step `kstep` into stage buffer `buf`.  Steps past k1 are still
+  // issued, with an out-of-range offset (the buffer returns zeros and moves no
+  // memory), so every step has the same number of loads in flight.
   auto issue = [&](int kstep, int buf) {
     bf16_t* at = smem + buf * STAGE;
     bf16_t* bt = at + A_EL;
-    const bool live = kstep < nk;
+    const bool live = kstep < k1;
 #pragma unroll
     for (int i = 0; i < LA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -698,16 +748,17 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
     }
   };
 
-  if (nk > 0) {
-    issue(0, 0);
-    issue(1, 1);
+  const int nks = k1 - k0;
+  if (nks > 0) {
+    issue(k0, 0);
+    issue(k0 + 1, 1);
     __builtin_amdgcn_s_waitcnt(kWaitStage0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     read_ks(0, 0, fa0, fb0);
-    for (int kt = 0; kt + 1 < nk; ++kt) {
-      const int cur = kt & 1;
+    for (int i = 0; i + 1 < nks; ++i) {
+      const int cur = i & 1;
       read_ks(cur, 1, fa1, fb1);
       mfma_ks(fa0, fb0);
       interleave(0);
@@ -717,19 +768,19 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
       read_ks(cur, 3, fa1, fb1);
       mfma_ks(fa0, fb0);
       interleave(0);
-      // publish stage kt+1; every wave's reads of stage kt have retired
+      // publish the next stage; every wave's reads of this one have retired
       __builtin_amdgcn_s_waitcnt(kWaitAll);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      // refill stage kt's buffer with stage kt+2, read k-step 0 of stage
-      // kt+1, run k-step 3 of stage kt
-      issue(kt + 2, cur);
+      // refill this stage's buffer two steps ahead, read k-step 0 of the next
+      // stage, run k-step 3 of this one
+      issue(k0 + i + 2, cur);
       read_ks(cur ^ 1, 0, fa0, fb0);
       mfma_ks(fa1, fb1);
       interleave(kLoads);
     }
-    const int last = (nk - 1) & 1;
+    const int last = (nks - 1) & 1;
     read_ks(last, 1, fa1, fb1);
     mfma_ks(fa0, fb0);
     read_ks(last, 2, fa0, fb0);
@@ -741,34 +792,166 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   wait_vmcnt_le(0);
   __syncthreads();
 
+  if (role == ROLE_PART) {
+    // publish the fp32 partial: coalesced 16-byte stores in register order.
+    // They are device-scope stores (sc1: written through to the level all
+    // XCDs share, as relaxed agent-scope atomic stores are), so completing
+    // them (vmcnt 0) is all that must precede the flag; no L2 write-back is
+    // needed.  Buffer stores take each store's offset from a scalar constant,
+    // so no address registers are kept per store.
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part + static_cast<int64_t>(slot) * NF * kThreads * 4,
+                                                NF * kThreads * 16);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4_t v = {acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
+                             acc[tm][tn][4 * q + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rp, tid * 16,
+                                                 ((tm * TN + tn) * 4 + q) * kThreads * 16, kDeviceScope);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one 32x32 tile of accumulator reads at a time
+      }
+    wait_vmcnt_le(0);
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(p.flags + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  if (role == ROLE_OWNER) {
+    // wait for the later part (a tile is cut at most once: every stream-K
+    // range is at least one tile long), which the staging below adds; the
+    // flag is cleared once consumed, so the flags are all zero again when the
+    // launch ends
+    if (tid == 0) {
+      int polls = 0;
+      while (__hip_atomic_load(p.flags + partner, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
+             ++polls < kSpinLimit)
+        __builtin_amdgcn_s_sleep(8);
+      __hip_atomic_store(p.flags + partner, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (polls >= kSpinLimit)  // never expected: report through the error word
+        __hip_atomic_store(p.flags + gridDim.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();  // the partial is read below with device-scope loads
+  }
+
   // epilogue: every wave stages its bf16 accumulators in the LDS C tile (one
   // 32x32 MFMA tile at a time; the scheduling barriers keep the compiler from
   // hoisting all accumulator reads, which would spill), then the block stores
   // the whole tile
+  // (an owner adds its partner's fp32 partial here, so the accumulators are
+  // only ever written by the MFMAs)
   bf16_t* Cs = smem;
   const int lr = lane & 31;
   const int lq = (lane >> 5) * 4;
+  const __amdgpu_buffer_rsrc_t rpart =
+      make_rsrc(p.part + static_cast<int64_t>(partner) * NF * kThreads * 4, NF * kThreads * 16);
+  auto stage = [&](auto add) {
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
-    const int ml = wm * WM + tm * 32 + lr;
+    for (int tm = 0; tm < TM; ++tm) {
+      const int ml = wm * WM + tm * 32 + lr;
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-      const int nl = tile_col(tn) + lq;
+      for (int tn = 0; tn < TN; ++tn) {
+        const int nl = tile_col(tn) + lq;
+        if constexpr (decltype(add)::value) {
+          f32x4_t pv[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<uint2*>(Cs + ml * LDC + nl + q * 8) =
-            pack4(acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
-                  acc[tm][tn][4 * q + 3]);
-      __builtin_amdgcn_sched_barrier(0);
+          for (int q = 0; q < 4; ++q)
+            pv[q] = __builtin_bit_cast(
+                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                             rpart, tid * 16, ((tm * TN + tn) * 4 + q) * kThreads * 16, kDeviceScope));
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<uint2*>(Cs + ml * LDC + nl + q * 8) =
+                pack4(acc[tm][tn][4 * q] + pv[q][0], acc[tm][tn][4 * q + 1] + pv[q][1],
+                      acc[tm][tn][4 * q + 2] + pv[q][2], acc[tm][tn][4 * q + 3] + pv[q][3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<uint2*>(Cs + ml * LDC + nl + q * 8) =
+                pack4(acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
+                      acc[tm][tn][4 * q + 3]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-  }
+  };
+  if (role == ROLE_OWNER) stage(std::true_type{});
+  else stage(std::false_type{});
   __syncthreads();
   store_c_tile<BM, BN, LDC, MODE, EPI>(p, Cs, e, m0, row_begin, row_end, n0, a0);
+  __syncthreads();  // the C tile is read before a next tile's loads refill the LDS
 }
 
+// One block per tile.
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
-  gemm_dl_body<BM, BN, A_KC, B_KC, MODE, EPI>(p);
+  const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
+  if (tile >= p.total_tiles) return;
+  TileCoord tc;
+  if constexpr (MODE == 0) tc = decode_rows_tile<BM, BN>(p, tile, p.m_tiles);
+  else tc = decode_k_tile<BM, BN>(p, tile);
+  if (!tc.valid) return;
+  gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
+}
+
+// Persistent grouped-rows GEMM, one block per CU (cooperative launch, so all
+// blocks are resident and a flag wait always ends).  The R x n_tiles tiles
+// (R = tile_offsets[E], read on the device) are split into whole-tile rounds
+// of G tiles, one per block, and a stream-K tail: the last T - (T/G - 1)*G
+// tiles' K steps are cut into G equal contiguous ranges, so every block gets
+// the same work and block epilogues fall at different times.  A tile cut
+// between blocks is finished by the block holding its first K step.
+template <int BM, int BN, bool A_KC, bool B_KC, int EPI>
+__device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
+  const int G = gridDim.x;
+  const int v = (G % 8 == 0) ? static_cast<int>(xcd_remap(blockIdx.x, G)) : static_cast<int>(blockIdx.x);
+  const int R = ld_const(p.tile_offsets, p.E);
+  const int64_t T = static_cast<int64_t>(R) * p.n_tiles;
+  const int nk = p.K / DL_BK;
+  if (T == 0 || nk == 0) return;
+  // whole-tile rounds (all tiles when there are at most G of them)
+  const int64_t rounds = T <= G ? 1 : T / G - 1;
+  const int64_t base = T <= G ? T : rounds * G;
+  const int64_t iters = (T - base) * nk;
+  const int64_t S = (iters + G - 1) / G;
+  int64_t r = 0;                 // next whole-tile round
+  int64_t g = v * S;             // next K step of the stream-K range
+  const int64_t gend = g + S < iters ? g + S : iters;
+  // one call site for every work item keeps a single copy of the tile code
+  for (;;) {
+    int64_t t;
+    int k0 = 0, k1 = nk, role = ROLE_FULL;
+    if (r < rounds) {
+      t = r * G + v;
+      ++r;
+      if (t >= base) continue;
+    } else if (g < gend) {
+      const int64_t ts = g / nk;
+      k0 = static_cast<int>(g - ts * nk);
+      const int64_t rest = gend - g;
+      k1 = rest < nk - k0 ? k0 + static_cast<int>(rest) : nk;
+      if (k0 > 0) {
+        role = ROLE_PART;  // a block's first range only
+      } else if (k1 < nk) {
+        role = ROLE_OWNER;  // block v + 1 holds K steps [k1, nk) of this tile
+      }
+      t = base + ts;
+      g += k1 - k0;
+    } else {
+      break;
+    }
+    const TileCoord tc = decode_rows_tile<BM, BN>(p, t, R);
+    gemm_dl_tile<BM, BN, A_KC, B_KC, 0, EPI>(p, tc, k0, k1, role, v, v + 1);
+  }
+#endif
+}
+
+template <int BM, int BN, bool A_KC, bool B_KC, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs p) {
+  gemm_sk_body<BM, BN, A_KC, B_KC, EPI>(p);
 }
 
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
@@ -792,12 +975,51 @@ static int launch(const GemmArgs& a, hipStream_t st, const char* name) {
   return clear_error();
 }
 
+// Persistent blocks per device: one per CU.
+constexpr int kMaxSkBlocks = 1023;
+constexpr int kSkMinK = 4096;
+constexpr int64_t kSkFlagBytes = 4096;  // int32 flags [G] + error word, zero on entry
+constexpr int64_t kSkSlotBytes = 256 * 256 * 4;  // fp32 partial of the largest tile
+
+static int sk_blocks() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = cus < kMaxSkBlocks ? cus : kMaxSkBlocks;
+  }
+  return cached[dev];
+}
+
+template <int BM, int BN, bool B_KC, int EPI>
+static int launch_sk(GemmArgs a, void* ws, hipStream_t st, const char* name) {
+  if (a.total_tiles <= 0) return clear_error();
+  // The persistent schedule costs some per-tile efficiency (measured ~10%)
+  // and moves fp32 partials for cut tiles; it pays where a tile is long
+  // (K >= kSkMinK), so a mostly empty last round of whole tiles costs more.
+  if (ws == nullptr || a.K % DL_BK != 0 || a.K < kSkMinK || !g_use_tr)
+    return launch<BM, BN, true, B_KC, 0, EPI>(a, st, name);
+  const int G = sk_blocks();
+  if (G <= 0) return set_error(std::string(name) + ": cannot query the CU count");
+  a.flags = static_cast<int*>(ws);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kSkFlagBytes);
+  void* args[] = {&a};
+  const hipError_t err = hipLaunchCooperativeKernel(
+      reinterpret_cast<const void*>(&gemm_sk_kernel<BM, BN, true, B_KC, EPI>), dim3(G),
+      dim3(kThreads), args, 0, st);
+  if (err != hipSuccess)
+    return set_error(std::string(name) + ": cooperative launch failed: " + hipGetErrorString(err));
+  return clear_error();
+}
+
 // Grouped-rows launch with the row-tile height the caller's tile_offsets were
 // computed for.
 template <int BN, bool B_KC, int EPI>
-static int launch_rows(const GemmArgs& a, int tile_rows, hipStream_t st, const char* name) {
-  if (tile_rows == 256) return launch<256, BN, true, B_KC, 0, EPI>(a, st, name);
-  return launch<128, BN, true, B_KC, 0, EPI>(a, st, name);
+static int launch_rows(const GemmArgs& a, int tile_rows, void* ws, hipStream_t st, const char* name) {
+  if (tile_rows == 256) return launch_sk<256, BN, B_KC, EPI>(a, ws, st, name);
+  return launch_sk<128, BN, B_KC, EPI>(a, ws, st, name);
 }
 
 static GemmArgs rows_args(const int32_t* offsets, const int32_t* tile_offsets, int E,
@@ -830,6 +1052,11 @@ extern "C" int ffmoe_gemm_tile_rows(int64_t max_rows, int E) {
   return (E > 0 && max_rows / E >= 384) ? 256 : 128;
 }
 
+extern "C" int64_t ffmoe_gemm_workspace_bytes(void) {
+  const int G = sk_blocks();
+  return G > 0 ? kSkFlagBytes + static_cast<int64_t>(G) * kSkSlotBytes : -1;
+}
+
 extern "C" int ffmoe_set_lds_transpose(int enable) {
   const int prev = g_use_tr;
   g_use_tr = enable ? 1 : 0;
@@ -839,7 +1066,7 @@ extern "C" int ffmoe_set_lds_transpose(int enable) {
 extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const int32_t* offsets,
                                  const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
                                  int D, int H, int activation, void* up_out, void* act_out,
-                                 void* stream) {
+                                 void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_up_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > 2) return set_error("ffmoe_gemm_up_glu: unknown activation");
   constexpr int BN = 256;
@@ -856,12 +1083,12 @@ extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const i
   a.K = D;
   a.H = H;
   a.act = activation;
-  return launch_rows<BN, true, EPI_GLU_FWD>(a, tile_rows, static_cast<hipStream_t>(stream), "gemm_up_glu");
+  return launch_rows<BN, true, EPI_GLU_FWD>(a, tile_rows, sk_workspace, static_cast<hipStream_t>(stream), "gemm_up_glu");
 }
 
 extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
                                const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
-                               int H, int D, void* down_out, void* stream) {
+                               int H, int D, void* down_out, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_down", E, max_rows, D, H, tile_rows)) return 1;
   constexpr int BN = 256;
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
@@ -874,13 +1101,13 @@ extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_
   a.b_stride = static_cast<int64_t>(D) * H;
   a.N = D;
   a.K = H;
-  return launch_rows<BN, true, EPI_STORE>(a, tile_rows, static_cast<hipStream_t>(stream), "gemm_down");
+  return launch_rows<BN, true, EPI_STORE>(a, tile_rows, sk_workspace, static_cast<hipStream_t>(stream), "gemm_down");
 }
 
 extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,
                                     const int32_t* offsets, const int32_t* tile_offsets,
                                     int tile_rows, int E, int64_t max_rows, int D, int H,
-                                    int activation, void* gup_out, void* stream) {
+                                    int activation, void* gup_out, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > 2) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
   constexpr int BN = 256;
@@ -897,13 +1124,13 @@ extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const v
   a.K = D;
   a.H = H;
   a.act = activation;
-  return launch_rows<BN, false, EPI_GLU_BWD>(a, tile_rows, static_cast<hipStream_t>(stream),
+  return launch_rows<BN, false, EPI_GLU_BWD>(a, tile_rows, sk_workspace, static_cast<hipStream_t>(stream),
                                              "gemm_dgrad_glu");
 }
 
 extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t* offsets,
                                 const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
-                                int H, int D, void* ghb_out, void* stream) {
+                                int H, int D, void* ghb_out, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad", E, max_rows, D, H, tile_rows)) return 1;
   constexpr int BN = 256;
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
@@ -916,7 +1143,7 @@ extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t
   a.b_stride = static_cast<int64_t>(2) * H * D;
   a.N = D;
   a.K = 2 * H;
-  return launch_rows<BN, false, EPI_STORE>(a, tile_rows, static_cast<hipStream_t>(stream), "gemm_dgrad");
+  return launch_rows<BN, false, EPI_STORE>(a, tile_rows, sk_workspace, static_cast<hipStream_t>(stream), "gemm_dgrad");
 }
 
 extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* offsets, int E, int M,

@@ -112,18 +112,48 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     const bool row_ok = row < ntok;
     const bf16_t* xr = x + (tok_base + (row_ok ? row : 0)) * static_cast<int64_t>(D);
     const int kq = (lane >> 4) * 8;
-    for (int k0 = 0; k0 < D; k0 += 32) {
-      const int kk = k0 + kq;
-      uint4 av = make_uint4(0, 0, 0, 0);
-      if (row_ok && kk < D) av = *reinterpret_cast<const uint4*>(xr + kk);
-      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
+    // batches of U k-steps: all of a batch's x loads (and, for few experts,
+    // gate loads) are in flight together instead of one latency per k-step
+    constexpr int U = 8;
+    for (int k0 = 0; k0 < D; k0 += 32 * U) {
+      uint4 av[U];
 #pragma unroll
-      for (int t = 0; t < ET; ++t) {
-        const int e = 16 * t + (lane & 15);
-        uint4 bv = make_uint4(0, 0, 0, 0);
-        if (e < E && kk < D) bv = *reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(e) * D + kk);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv),
-                                                        acc[t], 0, 0, 0);
+      for (int u = 0; u < U; ++u) {
+        const int kk = k0 + 32 * u + kq;
+        av[u] = make_uint4(0, 0, 0, 0);
+        if (row_ok && kk < D) av[u] = *reinterpret_cast<const uint4*>(xr + kk);
+      }
+      if constexpr (ET <= 2) {
+        uint4 bv[U][ET];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int t = 0; t < ET; ++t) {
+            const int e = 16 * t + (lane & 15);
+            const int kk = k0 + 32 * u + kq;
+            bv[u][t] = make_uint4(0, 0, 0, 0);
+            if (e < E && kk < D) bv[u][t] = *reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(e) * D + kk);
+          }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int t = 0; t < ET; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[u]),
+                                                            __builtin_bit_cast(bf16x8_t, bv[u][t]),
+                                                            acc[t], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int t = 0; t < ET; ++t) {
+            const int e = 16 * t + (lane & 15);
+            const int kk = k0 + 32 * u + kq;
+            uint4 bv = make_uint4(0, 0, 0, 0);
+            if (e < E && kk < D) bv = *reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(e) * D + kk);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[u]),
+                                                            __builtin_bit_cast(bf16x8_t, bv), acc[t],
+                                                            0, 0, 0);
+          }
       }
     }
     // Output layout: lane l holds expert 16t + l%16 for tokens 4*(l/16) + r.
@@ -239,36 +269,63 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
 
 // Single block: per-expert prefix over route blocks (block bases replace the
 // histogram in place), counts, row offsets, GEMM tile offsets, losses and
-// routing metrics.
+// routing metrics.  The 256 threads are split into E groups of G threads;
+// thread g of expert e owns a contiguous run of route blocks, so the scan is
+// a per-thread sum, a prefix over the G partial sums, then a second pass
+// writing the bases.  Every sum has a fixed order (deterministic).
 __global__ __launch_bounds__(256) void route_scan_kernel(
     int64_t N, int64_t nblk, int E, int k, int mt, int bm, float aux_coeff, float z_coeff,
     int gating, RouteWs ws, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ tile_offsets, float* __restrict__ stats, int32_t* __restrict__ istats) {
+    int32_t* __restrict__ tile_offsets, float* __restrict__ stats, int32_t* __restrict__ istats,
+    float* __restrict__ aux_out, float* __restrict__ z_out) {
+  __shared__ int s_part[256];
+  __shared__ float s_fpart[256];
+  __shared__ float s_z[256];
   __shared__ int s_rows[FFMOE_MAX_EXPERTS];
   __shared__ int s_tiles[FFMOE_MAX_EXPERTS];
   __shared__ int s_cnt[FFMOE_MAX_EXPERTS];
   __shared__ float s_fp[FFMOE_MAX_EXPERTS];
-  const int e = threadIdx.x;
-  if (e < E) {
-    int run = 0;
-    float ps = 0.0f, ss = 0.0f;
-    for (int64_t b = 0; b < nblk; ++b) {
+  const int tid = threadIdx.x;
+  const int G = 256 / E;  // threads per expert (E <= 256)
+  const int e = tid / G, g = tid % G;
+  const bool active = e < E;
+  const int64_t chunk = (nblk + G - 1) / G;
+  const int64_t b0 = active ? min<int64_t>(nblk, g * chunk) : 0;
+  const int64_t b1 = active ? min<int64_t>(nblk, b0 + chunk) : 0;
+  int run = 0;
+  float ps = 0.0f;
+  for (int64_t b = b0; b < b1; ++b) {
+    run += ws.hist[b * E + e];
+    ps += (gating == FFMOE_GATING_SOFTMAX) ? ws.psum[b * E + e] : ws.ssum[b * E + e];
+  }
+  s_part[tid] = run;
+  s_fpart[tid] = ps;
+  // z: strided partial sums, reduced below in thread order
+  float z = 0.0f;
+  for (int64_t b = tid; b < nblk; b += 256) z += ws.zpart[b];
+  s_z[tid] = z;
+  __syncthreads();
+  if (active) {
+    int base = 0;
+    for (int q = 0; q < g; ++q) base += s_part[e * G + q];
+    for (int64_t b = b0; b < b1; ++b) {
       const int c = ws.hist[b * E + e];
-      ws.hist[b * E + e] = run;
-      run += c;
-      ps += ws.psum[b * E + e];
-      if (gating == FFMOE_GATING_SIGMOID) ss += ws.ssum[b * E + e];
+      ws.hist[b * E + e] = base;
+      base += c;
     }
-    counts[e] = run;
-    s_cnt[e] = run;
-    const int rows = min(run, mt);
-    s_rows[e] = rows;
-    s_tiles[e] = (rows + bm - 1) / bm;
-    const float P = (gating == FFMOE_GATING_SOFTMAX ? ps : ss) / static_cast<float>(N);
-    s_fp[e] = (static_cast<float>(run) / static_cast<float>(N)) * P;
+    if (g == G - 1) {  // base is now the expert's total
+      float P = 0.0f;
+      for (int q = 0; q < G; ++q) P += s_fpart[e * G + q];
+      counts[e] = base;
+      s_cnt[e] = base;
+      const int rows = min(base, mt);
+      s_rows[e] = rows;
+      s_tiles[e] = (rows + bm - 1) / bm;
+      s_fp[e] = (static_cast<float>(base) / static_cast<float>(N)) * (P / static_cast<float>(N));
+    }
   }
   __syncthreads();
-  if (e == 0) {
+  if (tid == 0) {
     int ro = 0, to = 0, mx = 0, mn = 0x7fffffff, dropped = 0;
     int64_t tot = 0;
     float fp = 0.0f;
@@ -285,10 +342,12 @@ __global__ __launch_bounds__(256) void route_scan_kernel(
     }
     offsets[E] = ro;
     tile_offsets[E] = to;
-    float z = 0.0f;
-    for (int64_t b = 0; b < nblk; ++b) z += ws.zpart[b];
+    float zt = 0.0f;
+    for (int q = 0; q < 256; ++q) zt += s_z[q];
     stats[FFMOE_STAT_AUX] = aux_coeff * static_cast<float>(E) * fp;
-    stats[FFMOE_STAT_Z] = z_coeff * (z / static_cast<float>(N));
+    stats[FFMOE_STAT_Z] = z_coeff * (zt / static_cast<float>(N));
+    if (aux_out != nullptr) *aux_out = stats[FFMOE_STAT_AUX];
+    if (z_out != nullptr) *z_out = stats[FFMOE_STAT_Z];
     const float mean = static_cast<float>(tot) / static_cast<float>(E);
     stats[FFMOE_STAT_IMBALANCE] = static_cast<float>(mx) / (mean + 1e-6f);
     stats[FFMOE_STAT_DROP_FRAC] = static_cast<float>(dropped) / static_cast<float>(N * k);
@@ -458,13 +517,13 @@ extern "C" int ffmoe_route_fwd(const void* x, const void* gate, const void* logi
 extern "C" int ffmoe_route_scan(int64_t N, int E, int k, int mt, int gemm_bm, float aux_coeff,
                                 float z_coeff, int gating, void* workspace, int32_t* counts,
                                 int32_t* offsets, int32_t* tile_offsets, float* stats,
-                                int32_t* istats, void* stream) {
+                                int32_t* istats, float* aux_out, float* z_out, void* stream) {
   if (N <= 0 || E < 1 || E > FFMOE_MAX_EXPERTS) return set_error("ffmoe_route_scan: bad N/E");
   if (mt < 0 || gemm_bm <= 0) return set_error("ffmoe_route_scan: bad mt/gemm_bm");
   RouteWs ws = route_ws(workspace, N, E);
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), N,
                      route_blocks(N), E, k, mt, gemm_bm, aux_coeff, z_coeff, gating, ws, counts,
-                     offsets, tile_offsets, stats, istats);
+                     offsets, tile_offsets, stats, istats, aux_out, z_out);
   if (check_launch("route_scan_kernel")) return 1;
   return clear_error();
 }

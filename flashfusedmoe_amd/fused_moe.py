@@ -123,8 +123,8 @@ class _FusedMoEFunction(torch.autograd.Function):
         act_id = L.ACTIVATION[activation]
         need_ssum = gating == "sigmoid" and aux_coeff > 0.0
 
-        (logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats,
-         ws) = ops.route(xc, gc, expert_bias, top_k, gate_id, mt, float(aux_coeff),
+        (logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats, ws, aux,
+         z) = ops.route(xc, gc, expert_bias, top_k, gate_id, mt, float(aux_coeff),
                          float(z_coeff), need_ssum)
 
         if not capacity_mode and not allow_dropped:
@@ -135,13 +135,14 @@ class _FusedMoEFunction(torch.autograd.Function):
         out, tw, row_of, xs, up, act, down = ops.experts_forward(
             xc, wu, wd, topk_idx, topk_w, counts, offsets, tile_offsets, ws, top_k, act_id, mt,
             capacity_mode, not recompute)
+        if not capacity_mode:
+            tw = topk_w
 
         ctx.cfg = (top_k, act_id, gate_id, capacity_mode, float(aux_coeff), float(z_coeff))
         ctx.in_dtypes = (x.dtype, gate.dtype, w_up.dtype, w_down.dtype)
         ctx.save_for_backward(xc, gc, wu, wd, logits, topk_idx, tw, lse, counts, offsets,
                               tile_offsets, row_of, xs, up, act, down)
-        aux = stats[L.STAT_AUX].clone()
-        z = stats[L.STAT_Z].clone()
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled gradients
         ctx.aux_has_grad = gating == "sigmoid"
         non_diff = [topk_idx, counts, stats, istats]
         if not ctx.aux_has_grad:

@@ -41,7 +41,9 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
           mt: int, aux_coeff: float, z_coeff: float, need_ssum: bool) -> List[Tensor]:
     """Returns [logits bf16 [N,E], topk_idx int64 [N,k], topk_w fp32 [N,k],
     lse fp32 [N], counts int32 [E], offsets int32 [E+1], tile_offsets int32
-    [E+1], stats fp32 [4], istats int32 [4], workspace uint8]."""
+    [E+1], stats fp32 [4], istats int32 [4], workspace uint8, aux_loss fp32 [],
+    z_loss fp32 []] (the two losses repeat stats[AUX] and stats[Z] as
+    separate tensors)."""
     _check_bf16_gpu("hidden_states", x)
     _check_bf16_gpu("gate_weight", gate)
     N, D = x.shape
@@ -58,6 +60,8 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
     tile_offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
     stats = torch.empty(L.NUM_STATS, dtype=torch.float32, device=dev)
     istats = torch.empty(L.NUM_ISTATS, dtype=torch.int32, device=dev)
+    aux = torch.empty((), dtype=torch.float32, device=dev)
+    z = torch.empty((), dtype=torch.float32, device=dev)
     bias = None
     if expert_bias is not None:
         bias = expert_bias.to(device=dev, dtype=torch.float32).contiguous()
@@ -66,8 +70,8 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
            int(need_ssum), L.ptr(logits), L.ptr(topk_idx), L.ptr(topk_w), L.ptr(lse), L.ptr(ws), st)
     L.call("ffmoe_route_scan", N, E, k, mt, L.gemm_tile_rows(N * k, E), aux_coeff, z_coeff, gating,
            L.ptr(ws), L.ptr(counts), L.ptr(offsets), L.ptr(tile_offsets), L.ptr(stats),
-           L.ptr(istats), st)
-    return [logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats, ws]
+           L.ptr(istats), L.ptr(aux), L.ptr(z), st)
+    return [logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats, ws, aux, z]
 
 
 @route.register_fake
@@ -78,7 +82,8 @@ def _route_fake(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, nee
     return [f(N, E, dtype=_BF16), f(N, top_k, dtype=torch.int64), f(N, top_k, dtype=torch.float32),
             f(N, dtype=torch.float32), f(E, dtype=torch.int32), f(E + 1, dtype=torch.int32),
             f(E + 1, dtype=torch.int32), f(L.NUM_STATS, dtype=torch.float32),
-            f(L.NUM_ISTATS, dtype=torch.int32), f(0, dtype=torch.uint8)]
+            f(L.NUM_ISTATS, dtype=torch.int32), f(0, dtype=torch.uint8), f(dtype=torch.float32),
+            f(dtype=torch.float32)]
 
 
 # ---------------------------------------------------------------------------
@@ -94,10 +99,11 @@ def _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, save_up, st):
     act = torch.empty(T, H, dtype=_BF16, device=dev)
     down = torch.empty(T, D, dtype=_BF16, device=dev)
     tr = L.gemm_tile_rows(T, E)
+    ws = L.ptr(L.gemm_workspace(dev, st))
     L.call("ffmoe_gemm_up_glu", L.ptr(xs), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
-           T, D, H, activation, L.ptr(up), L.ptr(act), st)
+           T, D, H, activation, L.ptr(up), L.ptr(act), ws, st)
     L.call("ffmoe_gemm_down", L.ptr(act), L.ptr(w_down), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
-           T, H, D, L.ptr(down), st)
+           T, H, D, L.ptr(down), ws, st)
     return up, act, down
 
 
@@ -106,8 +112,9 @@ def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, t
                     counts: Tensor, offsets: Tensor, tile_offsets: Tensor, ws: Tensor, top_k: int,
                     activation: int, mt: int, capacity_mode: bool,
                     save_activations: bool) -> List[Tensor]:
-    """Returns [out bf16 [N,D], topk_w fp32 [N,k] (renormalised under capacity
-    dropping), row_of int32 [N*k], x_sorted bf16 [N*k,D], up, act, down] where
+    """Returns [out bf16 [N,D], topk_w fp32 [N,k] renormalised under capacity
+    dropping (empty without capacity: the weights are topk_w unchanged),
+    row_of int32 [N*k], x_sorted bf16 [N*k,D], up, act, down] where
     up/act/down are empty when save_activations is False."""
     _check_bf16_gpu("w_up", w_up)
     _check_bf16_gpu("w_down", w_down)
@@ -117,7 +124,7 @@ def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, t
     T = N * k
     dev = x.device
     st = L.stream_ptr(dev)
-    tw = topk_w.clone()
+    tw = topk_w.clone() if capacity_mode else topk_w
     xs = torch.empty(T, D, dtype=_BF16, device=dev)
     row_of = torch.empty(T, dtype=torch.int32, device=dev)
     L.call("ffmoe_permute", L.ptr(x), L.ptr(topk_idx), L.ptr(tw), L.ptr(offsets), L.ptr(counts),
@@ -126,10 +133,11 @@ def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, t
                              save_activations, st)
     out = torch.empty(N, D, dtype=_BF16, device=dev)
     L.call("ffmoe_combine", L.ptr(down), L.ptr(row_of), L.ptr(tw), None, N, D, k, L.ptr(out), st)
+    tw_out = tw if capacity_mode else topk_w.new_empty(0)
     empty = x.new_empty(0)
     if not save_activations:
-        return [out, tw, row_of, xs, empty, empty.clone(), empty.clone()]
-    return [out, tw, row_of, xs, up, act, down]
+        return [out, tw_out, row_of, xs, empty, empty.clone(), empty.clone()]
+    return [out, tw_out, row_of, xs, up, act, down]
 
 
 @experts_forward.register_fake
@@ -143,7 +151,8 @@ def _experts_forward_fake(x, w_up, w_down, topk_idx, topk_w, counts, offsets, ti
         acts = [e(T, H2), e(T, H2 // 2), e(T, D)]
     else:
         acts = [e(0), e(0), e(0)]
-    return [e(N, D), topk_w.new_empty(topk_w.shape), e(T, dtype=torch.int32), e(T, D), *acts]
+    tw = topk_w.new_empty(topk_w.shape) if capacity_mode else topk_w.new_empty(0)
+    return [e(N, D), tw, e(T, dtype=torch.int32), e(T, D), *acts]
 
 
 # ---------------------------------------------------------------------------
@@ -179,20 +188,32 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
            None, st)
     gup = torch.empty(T, H2, dtype=_BF16, device=dev)
     tr = L.gemm_tile_rows(T, E)
+    ws = L.ptr(L.gemm_workspace(dev, st))
     L.call("ffmoe_gemm_dgrad_glu", L.ptr(wgo), L.ptr(w_down), L.ptr(up), L.ptr(offsets),
-           L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(gup), st)
+           L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(gup), ws, st)
     ghb = torch.empty(T, D, dtype=_BF16, device=dev)
     L.call("ffmoe_gemm_dgrad", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
-           T, H, D, L.ptr(ghb), st)
-    # the two small dense gate products are plain library GEMMs (hipBLASLt)
-    addend = torch.matmul(gl, gate)
+           T, H, D, L.ptr(ghb), ws, st)
     dx = torch.empty(N, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_combine", L.ptr(ghb), L.ptr(row_of), None, L.ptr(addend), N, D, k, L.ptr(dx), st)
+    fused_gate = E <= L.MAX_FUSED_GATE_E
+    if fused_gate:  # the gl @ gate term is computed inside the dX reduce
+        L.call("ffmoe_dx_reduce", L.ptr(ghb), L.ptr(row_of), L.ptr(gl), L.ptr(gate), N, D, E, k,
+               L.ptr(dx), st)
+    else:  # many experts: the dense product is a plain library GEMM (hipBLASLt)
+        addend = torch.matmul(gl, gate)
+        L.call("ffmoe_combine", L.ptr(ghb), L.ptr(row_of), None, L.ptr(addend), N, D, k, L.ptr(dx),
+               st)
     dwd = torch.empty(E, D, H, dtype=_BF16, device=dev)
     L.call("ffmoe_gemm_wgrad", L.ptr(wgo), L.ptr(act), L.ptr(offsets), E, D, H, L.ptr(dwd), st)
     dwu = torch.empty(E, H2, D, dtype=_BF16, device=dev)
     L.call("ffmoe_gemm_wgrad", L.ptr(gup), L.ptr(xs), L.ptr(offsets), E, H2, D, L.ptr(dwu), st)
-    dgate = torch.matmul(gl.t().contiguous(), x)
+    if fused_gate:
+        dgate = torch.empty(E, D, dtype=_BF16, device=dev)
+        part = torch.empty(int(L.load().ffmoe_gate_grad_workspace_bytes(N, D, E)), dtype=torch.uint8,
+                           device=dev)
+        L.call("ffmoe_gate_grad", L.ptr(gl), L.ptr(x), N, D, E, L.ptr(part), L.ptr(dgate), st)
+    else:
+        dgate = torch.matmul(gl.t().contiguous(), x)
     return [dx, dgate, dwu, dwd]
 
 

@@ -51,6 +51,9 @@ extern "C" {
 /* limits enforced by the entry points */
 #define FFMOE_MAX_EXPERTS 256
 #define FFMOE_MAX_TOPK 16
+/* Largest expert count for which the gate-gradient products run in the
+ * fused kernels below (ffmoe_dx_reduce, ffmoe_gate_grad). */
+#define FFMOE_MAX_FUSED_GATE_E 32
 
 /* layout of the `stats` output of ffmoe_route_scan (fp32 slots) */
 #define FFMOE_STAT_AUX 0          /* aux_loss (coefficient applied)            */
@@ -112,12 +115,13 @@ int ffmoe_route_fwd(const void* x, const void* gate, const void* logits_in,
  *   number of gemm_bm-row tiles of experts < e.
  * Outputs: counts [E] int32 (tokens_per_expert), offsets [E+1] int32,
  *   tile_offsets [E+1] int32, stats [FFMOE_NUM_STATS] fp32,
- *   istats [FFMOE_NUM_ISTATS] int32. */
+ *   istats [FFMOE_NUM_ISTATS] int32.  * aux_out / z_out (may be NULL): single-float copies of stats[AUX] and
+ *   stats[Z], so a caller can hand the losses out as separate tensors. */
 int ffmoe_route_scan(int64_t N, int E, int k, int mt, int gemm_bm,
                      float aux_coeff, float z_coeff, int gating,
                      void* workspace, int32_t* counts, int32_t* offsets,
                      int32_t* tile_offsets, float* stats, int32_t* istats,
-                     void* stream);
+                     float* aux_out, float* z_out, void* stream);
 
 /* Stable permutation of tokens into expert-sorted compact rows.
  * Replaces: `fused_routing_scatter` (moe_ops.py:43-149) and the capacity
@@ -145,6 +149,16 @@ int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
  * expert to max_tokens rows). */
 int ffmoe_gemm_tile_rows(int64_t max_rows, int E);
 
+/* Bytes of the `sk_workspace` the four grouped-rows GEMMs below take on the
+ * current device (-1 if the device cannot be queried).  Its first 4 KiB are
+ * int32 flags that must be zero before the first call; every call leaves them
+ * zero again, so one workspace serves any number of calls in stream order.
+ * Calls that may overlap (different streams) need separate workspaces.
+ * With sk_workspace NULL the GEMMs run one block per tile instead of the
+ * persistent one-block-per-CU schedule whose last round is split along K.
+ * No reference counterpart (the reference's GEMMs are cuBLAS bmm calls). */
+int64_t ffmoe_gemm_workspace_bytes(void);
+
 /* up = x_sorted · w_up[e]^T and the fused GLU:
  *   up_out [rows, 2H] (pre-activation, may be NULL), act_out [rows, H].
  * Replaces: up bmm (fused_moe.py:435) + `activation_forward`
@@ -153,13 +167,15 @@ int ffmoe_gemm_tile_rows(int64_t max_rows, int E);
 int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up,
                       const int32_t* offsets, const int32_t* tile_offsets,
                       int tile_rows, int E, int64_t max_rows, int D, int H,
-                      int activation, void* up_out, void* act_out, void* stream);
+                      int activation, void* up_out, void* act_out, void* sk_workspace,
+                      void* stream);
 
 /* down [rows, D] = act · w_down[e]^T.  w_down [E, D, H].
  * Replaces: down bmm (fused_moe.py:441). */
 int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
                     const int32_t* tile_offsets, int tile_rows, int E,
-                    int64_t max_rows, int H, int D, void* down_out, void* stream);
+                    int64_t max_rows, int H, int D, void* down_out, void* sk_workspace,
+                    void* stream);
 
 /* gup [rows, 2H] = GLU_backward(wgo · w_down[e], up).
  * Replaces: dX-down bmm (fused_moe.py:547) + `activation_backward`
@@ -167,12 +183,13 @@ int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
 int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,
                          const int32_t* offsets, const int32_t* tile_offsets,
                          int tile_rows, int E, int64_t max_rows, int D, int H,
-                         int activation, void* gup_out, void* stream);
+                         int activation, void* gup_out, void* sk_workspace, void* stream);
 
 /* ghb [rows, D] = gup · w_up[e].  Replaces: dX-up bmm (fused_moe.py:553). */
 int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t* offsets,
                      const int32_t* tile_offsets, int tile_rows, int E,
-                     int64_t max_rows, int H, int D, void* ghb_out, void* stream);
+                     int64_t max_rows, int H, int D, void* ghb_out, void* sk_workspace,
+                     void* stream);
 
 /* Selects how MN-contiguous GEMM operands are read from LDS: 1 (default) =
  * ds_read_b64_tr_b16 transpose reads, 0 = element-wise reads.  Returns the
@@ -199,6 +216,24 @@ int ffmoe_gemm_wgrad(const void* a, const void* b, const int32_t* offsets, int E
 int ffmoe_combine(const void* rows, const int32_t* row_of, const float* topk_w,
                   const void* addend, int64_t N, int D, int k, void* out,
                   void* stream);
+
+/* dX reduce with the gate term: out[n] = bf16(bf16(sum_s ghb[row_of[n*k+s]])
+ *   + bf16(gl[n,:] . gate)), slot sum fp32 in slot order, gl . gate fp32 over
+ *   experts in index order.  gl [N,E] bf16, gate [E,D] bf16, E <=
+ *   FFMOE_MAX_FUSED_GATE_E.
+ * Replaces: the dX gather-reduce (fused_moe.py:556-561) and `gl @ gate`
+ *   added to it (fused_moe.py:590). */
+int ffmoe_dx_reduce(const void* ghb, const int32_t* row_of, const void* gl,
+                    const void* gate, int64_t N, int D, int E, int k, void* out,
+                    void* stream);
+
+/* Bytes of fp32 partials ffmoe_gate_grad needs for N tokens. */
+int64_t ffmoe_gate_grad_workspace_bytes(int64_t N, int D, int E);
+
+/* dgate [E,D] bf16 = gl^T · x, fp32 accumulation in a fixed order; E <=
+ * FFMOE_MAX_FUSED_GATE_E.  Replaces: `gl.t() @ hidden` (fused_moe.py:591). */
+int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, int E,
+                    void* workspace, void* dgate, void* stream);
 
 /* Routing backward, one pass per token.
  * Replaces: routing-weight grad (fused_moe.py:527-535), `fused_weighted_scatter`

@@ -51,7 +51,7 @@ def _route_from_logits(logits, k, gating, mt, capacity):
     istats = torch.empty(L.NUM_ISTATS, dtype=torch.int32, device=dev)
     L.call("ffmoe_route_scan", N, E, k, mt, L.gemm_tile_rows(N * k, E), 0.0, 0.0,
            L.GATING[gating], L.ptr(ws), L.ptr(counts), L.ptr(offsets), L.ptr(tiles),
-           L.ptr(stats), L.ptr(istats), st)
+           L.ptr(stats), L.ptr(istats), None, None, st)
     xs = torch.empty(max(N * k, 1), D, dtype=torch.bfloat16, device=dev)
     row_of = torch.empty(N * k, dtype=torch.int32, device=dev)
     tw = w.clone()

@@ -93,7 +93,7 @@ def test_permutation_bit_exact(N, E, k, mt, cap):
     if mt is None:
         mt = R.estimate_max_tokens(N, k, E)
     xg, gg, wug, wdg = cuda(x, gate, wu, wd)
-    (logits, idx, tw, lse, counts, offsets, tile_off, stats, istats, ws) = ops.route(
+    (logits, idx, tw, lse, counts, offsets, tile_off, stats, istats, ws, _aux, _z) = ops.route(
         xg, gg, None, k, 0, mt, 0.0, 0.0, False)
     out, tw2, row_of, xs, up, act, down = ops.experts_forward(
         xg, wug, wdg, idx, tw, counts, offsets, tile_off, ws, k, 0, mt, cap, True)
@@ -123,13 +123,18 @@ def _groups(E, sizes, D, H, seed):
     return xs, wu, wd, off
 
 
+# the skewed C2-sized case has more tiles than CUs, so the persistent
+# schedule splits tiles along K between blocks ("sk"); "dp" is one block per
+# tile, "elementwise" the element-wise LDS read variant of that
 @pytest.mark.parametrize("sizes,D,H", [
     ([300, 0, 128, 1, 513, 64, 0, 127], 256, 192),
     ([2048] * 8, 1024, 2048),
+    ([2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800], 1024, 2048),
+    ([2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800], 4096, 512),
     ([5, 17, 0, 260], 96, 40),
 ])
-@pytest.mark.parametrize("tr", [True, False])
-def test_grouped_gemms_against_fp32(sizes, D, H, tr, _lib):
+@pytest.mark.parametrize("mode", ["sk", "dp", "elementwise"])
+def test_grouped_gemms_against_fp32(sizes, D, H, mode, _lib):
     L = _lib
     E = len(sizes)
     xs, wu, wd, off = _groups(E, sizes, D, H, seed=sum(sizes) + D)
@@ -142,22 +147,24 @@ def test_grouped_gemms_against_fp32(sizes, D, H, tr, _lib):
     off_g = torch.from_numpy(off).to(dev)
     til_g = torch.from_numpy(tiles).to(dev)
     st = L.stream_ptr()
-    L.set_lds_transpose(tr)
+    L.set_lds_transpose(mode != "elementwise")
+    wsb = L.gemm_workspace(torch.device(dev), st)
+    ws = wsb.data_ptr() if mode == "sk" else None
     up = torch.empty(T, 2 * H, dtype=torch.bfloat16, device=dev)
     act = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     down = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
     L.call("ffmoe_gemm_up_glu", xs_g.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
-           bm, E, T, D, H, 0, up.data_ptr(), act.data_ptr(), st)
+           bm, E, T, D, H, 0, up.data_ptr(), act.data_ptr(), ws, st)
     L.call("ffmoe_gemm_down", act.data_ptr(), wd_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
-           bm, E, T, H, D, down.data_ptr(), st)
+           bm, E, T, H, D, down.data_ptr(), ws, st)
     g = torch.Generator().manual_seed(5)
     wgo = torch.randn(T, D, generator=g).to(torch.bfloat16).cuda()
     gup = torch.empty(T, 2 * H, dtype=torch.bfloat16, device=dev)
     L.call("ffmoe_gemm_dgrad_glu", wgo.data_ptr(), wd_g.data_ptr(), up.data_ptr(), off_g.data_ptr(),
-           til_g.data_ptr(), bm, E, T, D, H, 0, gup.data_ptr(), st)
+           til_g.data_ptr(), bm, E, T, D, H, 0, gup.data_ptr(), ws, st)
     ghb = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
     L.call("ffmoe_gemm_dgrad", gup.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
-           bm, E, T, H, D, ghb.data_ptr(), st)
+           bm, E, T, H, D, ghb.data_ptr(), ws, st)
     dwd = torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
     L.call("ffmoe_gemm_wgrad", wgo.data_ptr(), act.data_ptr(), off_g.data_ptr(), E, D, H,
            dwd.data_ptr(), st)
@@ -166,6 +173,8 @@ def test_grouped_gemms_against_fp32(sizes, D, H, tr, _lib):
            dwu.data_ptr(), st)
     torch.cuda.synchronize()
     L.set_lds_transpose(True)
+    # every flag consumed (the workspace is reusable) and no wait timed out
+    assert int(wsb[:4096].view(torch.int32).abs().sum().item()) == 0
 
     # fp32 reference per expert on the GPU, from the kernels' own bf16 inputs
     f = lambda t: t.float()  # noqa: E731
@@ -187,6 +196,89 @@ def test_grouped_gemms_against_fp32(sizes, D, H, tr, _lib):
             check_close(dwu[e], f(gup[a:b]).t() @ f(xs_g[a:b]), f"dW_up[e={e}]")
         else:
             assert dwd[e].abs().max().item() == 0 and dwu[e].abs().max().item() == 0
+
+
+def test_persistent_schedule_is_deterministic(_lib):
+    # tiles split along K are summed in a fixed slot order: two runs agree
+    # bit for bit, and the workspace flags are left zero
+    L = _lib
+    sizes = [2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800]
+    D, H = 1024, 2048
+    E = len(sizes)
+    xs, wu, wd, off = _groups(E, sizes, D, H, seed=77)
+    T = xs.shape[0]
+    bm = L.gemm_tile_rows(T, E)
+    tiles = np.zeros(E + 1, dtype=np.int32)
+    tiles[1:] = np.cumsum([-(-s // bm) for s in sizes])
+    xs_g, wu_g, wd_g = cuda(xs, wu, wd)
+    off_g = torch.from_numpy(off).cuda()
+    til_g = torch.from_numpy(tiles).cuda()
+    st = L.stream_ptr()
+    wsb = L.gemm_workspace(torch.device("cuda"), st)
+    outs = []
+    for _ in range(2):
+        up = torch.empty(T, 2 * H, dtype=torch.bfloat16, device="cuda")
+        act = torch.empty(T, H, dtype=torch.bfloat16, device="cuda")
+        ghb = torch.empty(T, D, dtype=torch.bfloat16, device="cuda")
+        L.call("ffmoe_gemm_up_glu", xs_g.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(),
+               til_g.data_ptr(), bm, E, T, D, H, 0, up.data_ptr(), act.data_ptr(), wsb.data_ptr(), st)
+        L.call("ffmoe_gemm_dgrad", up.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(),
+               til_g.data_ptr(), bm, E, T, H, D, ghb.data_ptr(), wsb.data_ptr(), st)
+        torch.cuda.synchronize()
+        outs.append((up.cpu(), act.cpu(), ghb.cpu()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert int(wsb[:4096].view(torch.int32).abs().sum().item()) == 0
+
+
+@pytest.mark.parametrize("E", [3, 8, 32])
+def test_dx_reduce_and_gate_grad_against_fp32(E, _lib):
+    # dx[n] = bf16(bf16(sum_s ghb[row]) + bf16(gl[n] . gate)); dgate = gl^T x
+    L = _lib
+    N, D, k = 1000, 264, 2
+    g = torch.Generator().manual_seed(E)
+    T = N * k
+    ghb = torch.randn(T, D, generator=g).to(torch.bfloat16)
+    gl = (torch.randn(N, E, generator=g) * 0.1).to(torch.bfloat16)
+    gate = (torch.randn(E, D, generator=g) * 0.05).to(torch.bfloat16)
+    x = torch.randn(N, D, generator=g).to(torch.bfloat16)
+    row_of = torch.randperm(T, generator=g).to(torch.int32)
+    row_of[::37] = L.ROW_DROPPED
+    row_of[5::53] = L.ROW_ALIAS0
+    ghb_g, gl_g, gate_g, x_g, ro_g = cuda(ghb, gl, gate, x, row_of)
+    st = L.stream_ptr()
+    dx = torch.empty(N, D, dtype=torch.bfloat16, device="cuda")
+    L.call("ffmoe_dx_reduce", ghb_g.data_ptr(), ro_g.data_ptr(), gl_g.data_ptr(), gate_g.data_ptr(),
+           N, D, E, k, dx.data_ptr(), st)
+    part = torch.empty(int(L.load().ffmoe_gate_grad_workspace_bytes(N, D, E)), dtype=torch.uint8,
+                       device="cuda")
+    dgate = torch.empty(E, D, dtype=torch.bfloat16, device="cuda")
+    L.call("ffmoe_gate_grad", gl_g.data_ptr(), x_g.data_ptr(), N, D, E, part.data_ptr(),
+           dgate.data_ptr(), st)
+    torch.cuda.synchronize()
+    src = row_of.long().clone()
+    src[row_of == L.ROW_ALIAS0] = 0
+    valid = (row_of != L.ROW_DROPPED).view(N, k, 1).double()
+    rows = ghb.double()[src.clamp(min=0)].view(N, k, D) * valid
+    s = rows.sum(1).to(torch.bfloat16).double()
+    a = (gl.double() @ gate.double()).to(torch.bfloat16).double()
+    check_close(dx.cpu(), (s + a), "dx")
+    check_close(dgate.cpu(), gl.double().t() @ x.double(), "dgate")
+
+
+def test_many_experts_gate_products_use_library_path():
+    # E above the fused-kernel limit: gl @ gate and gl^T x go to hipBLASLt
+    N, D, ffn, E, k = 512, 128, 256, 64, 4
+    x, gate, wu, wd = seeded(N, D, ffn, E, seed=64)
+    go = torch.randn(N, D, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    out, losses, grads = _run_layer(x, gate, wu, wd, k, go, allow_dropped_tokens=True)
+    from flashfusedmoe_amd import ops
+    logits = ops.route(x.cuda(), gate.cuda(), None, k, 0, 1, 0.0, 0.0, False)[0].cpu()
+    ref, st = F_.forward(x, gate, wu, wd, k, allow_dropped_tokens=True, logits=logits)
+    check_close(out, ref, "output")
+    gr = F_.backward(st, go)
+    check_close(grads[0], gr["hidden"], "grad hidden")
+    check_close(grads[1], gr["gate"], "grad gate", atol=2e-3 * max(1.0, gr["gate"].abs().max().item()))
 
 
 def test_transpose_and_elementwise_lds_reads_agree(_lib):
