@@ -462,8 +462,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Direct-to-LDS pipeline (the main path): BK = 64, two LDS stages filled by
-// buffer_load_dwordx4 ... lds (each wave instruction writes 1 KiB of
+// Direct-to-LDS pipeline (the main path): BK = 64, a ring of two or three
+// LDS stages filled by buffer_load_dwordx4 ... lds (each wave instruction writes 1 KiB of
 // consecutive LDS; per-lane source addresses implement the swizzle;
 // out-of-range rows read as zero through the buffer descriptor's bounds).
 // Every row segment a stage loads is a whole 128-byte line (64 bf16 of a
@@ -478,9 +478,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 // Each 64-K stage is four MFMA k-steps of 16; operand fragments are
 // double-buffered in registers.  Before the last k-step of stage kt: wait for
 // stage kt+1's loads, one s_barrier, refill stage kt's buffer with stage
-// kt+2, read stage kt+1's first fragments, then run the last k-step.
+// kt+NS, read stage kt+1's first fragments, then run the last k-step.
 constexpr int DL_BK = 64;
-constexpr int kStages = 2;
+// Stages of the LDS ring: three where they fit in the 160 KiB of LDS (tiles
+// of at most 384 rows + columns), else two.
+template <int BM, int BN>
+constexpr int dl_stages() { return (BM + BN) <= 384 ? 3 : 2; }
 
 __device__ __forceinline__ void wait_vmcnt_le(int n) {
   // s_waitcnt with only the vector-memory count constrained (expcnt and
@@ -579,7 +582,9 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   constexpr int LA = BM * DL_BK / 8 / kThreads;  // 16-byte loads per thread per stage
   constexpr int LB = BN * DL_BK / 8 / kThreads;
   constexpr int LDC = BN + 8;                // C staging row stride
-  constexpr int SMEM = (kStages * STAGE > BM * LDC) ? kStages * STAGE : BM * LDC;
+  constexpr int NS = dl_stages<BM, BN>();
+  constexpr int SMEM = (NS * STAGE > BM * LDC) ? NS * STAGE : BM * LDC;
+  static_assert(SMEM * 2 <= 160 * 1024, "LDS budget");
   constexpr int NF = TM * TN * 4;            // fp32 partial: float4s per thread
   static_assert(EPI != EPI_GLU_FWD || (TN % 2 == 0), "GLU forward pairs gate/up tiles");
   __shared__ __attribute__((aligned(1024))) bf16_t smem[SMEM];
@@ -688,7 +693,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  static_assert(DL_BK == 64 && kStages == 2, "four MFMA k-steps per stage, two stages");
+  static_assert(DL_BK == 64, "four MFMA k-steps per stage");
   // MFMA operand fragments of one k-step (16 of K), double-buffered in
   // registers (sets F0 / F1): the reads of one set overlap the MFMAs of the
   // other.  k-step 0 of stage kt+1 is read right after the barrier that
@@ -732,10 +737,15 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   constexpr int NM = TM * TN;  // MFMAs per k-step
   constexpr int kLoads = LA + LB;  // loads per thread per stage
   static_assert(kLoads < 64, "vmcnt range");
-  // prologue: stage 0 landed (stage 1 may be in flight), LDS count free
-  constexpr int kWaitStage0 = (kLoads & 15) | ((kLoads >> 4) << 14) | 0x70 | 0xF00;
-  // in the loop: stage kt+1 landed and this wave's LDS reads retired
-  constexpr int kWaitAll = 0x0070;
+  static_assert((NS - 1) * kLoads < 64, "vmcnt range");
+  // prologue: stage 0 landed (the NS-1 later stages may be in flight), LDS
+  // count free
+  constexpr int kPro = (NS - 1) * kLoads;
+  constexpr int kWaitStage0 = (kPro & 15) | ((kPro >> 4) << 14) | 0x70 | 0xF00;
+  // in the loop: the next stage landed (the NS-2 after it may be in flight)
+  // and this wave's LDS reads retired
+  constexpr int kIn = (NS - 2) * kLoads;
+  constexpr int kWaitNext = (kIn & 15) | ((kIn >> 4) << 14) | 0x70;
 
   // Scheduling of one k-step region: pair each LDS read and each stage load
   // with an MFMA, so one wave per SIMD issues them in the MFMAs' shadow.
@@ -750,15 +760,15 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
 
   const int nks = k1 - k0;
   if (nks > 0) {
-    issue(k0, 0);
-    issue(k0 + 1, 1);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) issue(k0 + s, s);
     __builtin_amdgcn_s_waitcnt(kWaitStage0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     read_ks(0, 0, fa0, fb0);
+    int cur = 0;  // ring buffer of the stage being computed
     for (int i = 0; i + 1 < nks; ++i) {
-      const int cur = i & 1;
       read_ks(cur, 1, fa1, fb1);
       mfma_ks(fa0, fb0);
       interleave(0);
@@ -769,23 +779,24 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
       mfma_ks(fa0, fb0);
       interleave(0);
       // publish the next stage; every wave's reads of this one have retired
-      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      __builtin_amdgcn_s_waitcnt(kWaitNext);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      // refill this stage's buffer two steps ahead, read k-step 0 of the next
+      // refill this stage's buffer NS steps ahead, read k-step 0 of the next
       // stage, run k-step 3 of this one
-      issue(k0 + i + 2, cur);
-      read_ks(cur ^ 1, 0, fa0, fb0);
+      issue(k0 + i + NS, cur);
+      const int nxt = cur + 1 == NS ? 0 : cur + 1;
+      read_ks(nxt, 0, fa0, fb0);
       mfma_ks(fa1, fb1);
       interleave(kLoads);
+      cur = nxt;
     }
-    const int last = (nks - 1) & 1;
-    read_ks(last, 1, fa1, fb1);
+    read_ks(cur, 1, fa1, fb1);
     mfma_ks(fa0, fb0);
-    read_ks(last, 2, fa0, fb0);
+    read_ks(cur, 2, fa0, fb0);
     mfma_ks(fa1, fb1);
-    read_ks(last, 3, fa1, fb1);
+    read_ks(cur, 3, fa1, fb1);
     mfma_ks(fa0, fb0);
     mfma_ks(fa1, fb1);
   }
@@ -1090,7 +1101,7 @@ extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_
                                const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
                                int H, int D, void* down_out, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_down", E, max_rows, D, H, tile_rows)) return 1;
-  constexpr int BN = 256;
+  constexpr int BN = 128;  // 256 x 128 tiles: a three-stage LDS ring fits
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(act);
   a.B = static_cast<const bf16_t*>(w_down);
@@ -1110,7 +1121,7 @@ extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const v
                                     int activation, void* gup_out, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > 2) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
-  constexpr int BN = 256;
+  constexpr int BN = 128;  // 256 x 128 tiles: a three-stage LDS ring fits
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(wgo);
   a.B = static_cast<const bf16_t*>(w_down);
@@ -1132,7 +1143,7 @@ extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t
                                 const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
                                 int H, int D, void* ghb_out, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad", E, max_rows, D, H, tile_rows)) return 1;
-  constexpr int BN = 256;
+  constexpr int BN = 128;  // 256 x 128 tiles: a three-stage LDS ring fits
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(gup);
   a.B = static_cast<const bf16_t*>(w_up);
