@@ -60,6 +60,25 @@ def time_events(fn, reps):
     return s.elapsed_time(e) / reps
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "gemm_hbm_traffic_c2.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of each grouped GEMM at C2, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of
+    known size); {} when the summary is absent."""
+    out = {}
+    try:
+        for line in open(TRAFFIC_FILE):
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes":
+                out[parts[1]] = int(parts[2])
+    except OSError:
+        pass
+    return out
+
+
 def kernel_rates(c, x, gate, wu, wd, go, reps=20):
     """Times each hot kernel alone (launched through the C ABI) and returns
     {name: {ms, rate, unit, frac, work}} with algorithmic work per launch."""
@@ -244,7 +263,8 @@ def main():
     if dom_name:
         d = kernels[dom_name]
         roofline = dict(kernel=dom_name, bound="mfma", achieved=round(d["rate"], 2),
-                        peak=PEAK_BF16_TFLOPS, unit="TFLOP/s", frac=round(d["frac"], 4), traffic=None)
+                        peak=PEAK_BF16_TFLOPS, unit="TFLOP/s", frac=round(d["frac"], 4),
+                        traffic=measured_traffic().get(dom_name))
 
     cpu = None
     if not args.no_cpu:
