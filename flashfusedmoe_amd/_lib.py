@@ -35,6 +35,8 @@ SIGNATURES = {
     "ffmoe_version": (_I, []),
     "ffmoe_route_workspace_bytes": (ctypes.c_size_t, [_L, _I, _I]),
     "ffmoe_route_fwd": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "ffmoe_route_fwd_ex": (_I, [_P, _P, _P, _P, _I, _I, _F, _I, _I, _P, _L, _I, _I, _I, _I, _I, _P, _P,
+                                _P, _P, _P, _P]),
     "ffmoe_route_scan": (_I, [_L, _I, _I, _I, _I, _F, _F, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "ffmoe_permute": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "ffmoe_gemm_tile_rows": (_I, [_L, _I]),
@@ -51,6 +53,8 @@ SIGNATURES = {
     "ffmoe_gate_grad": (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
     "ffmoe_route_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I,
                              _I, _I, _P, _P, _P, _P]),
+    "ffmoe_route_bwd_ex": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I, _I, _I,
+                                _I, _P, _P, _I, _F, _P, _P, _P, _P]),
     "ffmoe_glu_fwd": (_I, [_P, _L, _I, _I, _P, _P]),
     "ffmoe_glu_bwd": (_I, [_P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_scatter_rows": (_I, [_P, _P, _P, _L, _I, _I, _L, _P, _P]),

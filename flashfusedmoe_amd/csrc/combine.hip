@@ -202,6 +202,18 @@ __global__ __launch_bounds__(256) void gate_grad_final_kernel(const float* __res
   if (q == 0 && i < total) out[i] = f32_to_bf16(((s[tid] + s[tid + 64]) + s[tid + 128]) + s[tid + 192]);
 }
 
+// The aux loss's routing when its gradient flows through the routing weights:
+// the reference's slow routing path (any of expert_bias, pre_softmax,
+// scoring_factor, n_group) computes the aux-loss weights with differentiable
+// torch ops (fused_moe.py:144-200, :1165-1189), softmax gating only.
+struct AuxRoute {
+  int through_weights;     // 1: add d aux / d logits through the weights
+  const int64_t* idx;      // the aux routing's top-k [N,k] (null: the dispatch routing)
+  const int32_t* counts;   // its per-expert counts (null: `counts`)
+  int pre_softmax;         // weights were renormalised softmax probabilities
+  float scoring;           // > 0: weights were scaled by scoring / top_k
+};
+
 // Routing backward, one wave per token n:
 //   g_w[s] = <down[src_s], go[n]> (fp32)                 fused_moe.py:527-535
 //   wgo[row_s] = bf16(go[n] * bf16(w_s)) for owned rows   moe_ops.py:248-288
@@ -214,8 +226,8 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
     const float* __restrict__ topk_w, const bf16_t* __restrict__ logits,
     const float* __restrict__ lse, const int32_t* __restrict__ counts,
     const float* __restrict__ g_aux, const float* __restrict__ g_z, float aux_coeff, float z_coeff,
-    int64_t N, int D, int E, int k, int gating, int capacity_mode, bf16_t* __restrict__ wgo,
-    bf16_t* __restrict__ gl, float* __restrict__ grad_w) {
+    int64_t N, int D, int E, int k, int gating, int capacity_mode, AuxRoute ar,
+    bf16_t* __restrict__ wgo, bf16_t* __restrict__ gl, float* __restrict__ grad_w) {
   const int lane = threadIdx.x & 63;
   const int64_t n = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -290,6 +302,70 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
     for (int s = 0; s < KMAX; ++s)
       if (s == lane) grad_w[n * k + s] = gw[s];
   }
+  // aux loss through the routing weights: d aux / d w[s] = g * c * E * f_e / N
+  // with f_e = counts[e] / N, back through the weight formula
+  float aux_sel[KMAX];  // contribution to gl at aux_ids[s] (softmax over selected)
+  int aux_ids[KMAX];
+  float aux_dp[KMAX];   // pre-softmax: d aux / d p at aux_ids[s]
+  float aux_t = 0.0f;   // pre-softmax: sum_s p_s dp_s
+  const bool aux_w = ar.through_weights && g_aux != nullptr && gating == FFMOE_GATING_SOFTMAX;
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    aux_sel[s] = 0.0f;
+    aux_dp[s] = 0.0f;
+    aux_ids[s] = -1;
+  }
+  if (aux_w) {
+    const int64_t* ai = ar.idx != nullptr ? ar.idx : topk_idx;
+    const int32_t* ac = ar.counts != nullptr ? ar.counts : counts;
+    const float A = (*g_aux) * aux_coeff * static_cast<float>(E) / static_cast<float>(N);
+    const float a = ar.scoring > 0.0f ? ar.scoring / static_cast<float>(k) : 1.0f;
+    float ga[KMAX], l[KMAX];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+      ga[s] = 0.0f;
+      l[s] = 0.0f;
+      if (s < k) {
+        aux_ids[s] = static_cast<int>(ai[n * k + s]);
+        ga[s] = A * (static_cast<float>(ac[aux_ids[s]]) / static_cast<float>(N));
+        l[s] = bf16_to_f32(logits[n * E + aux_ids[s]]);
+        mx = fmaxf(mx, l[s]);
+      }
+    }
+    if (!ar.pre_softmax) {  // w = a * softmax(selected logits)
+      float ws[KMAX], z = 0.0f, sg = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s) {
+        ws[s] = s < k ? expf(l[s] - mx) : 0.0f;
+        z += ws[s];
+      }
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s) {
+        ws[s] /= z;
+        sg += ws[s] * a * ga[s];
+      }
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s)
+        if (s < k) aux_sel[s] = ws[s] * (a * ga[s] - sg);
+    } else {  // w = a * p_sel / (sum p_sel + 1e-6), p = softmax over all experts
+      float p[KMAX], S = 0.0f, gp = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s) {
+        p[s] = s < k ? expf(l[s] - lse[n]) : 0.0f;
+        S += p[s];
+        gp += ga[s] * p[s];
+      }
+      const float d = S + 1e-6f;
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s) {
+        if (s < k) {
+          aux_dp[s] = a * (ga[s] / d - gp / (d * d));
+          aux_t += p[s] * aux_dp[s];
+        }
+      }
+    }
+  }
   const float zc = (g_z != nullptr) ? (*g_z) * z_coeff * 2.0f * lse[n] / static_cast<float>(N) : 0.0f;
   const float ac = (g_aux != nullptr && gating == FFMOE_GATING_SIGMOID)
                        ? (*g_aux) * aux_coeff * static_cast<float>(E) / static_cast<float>(N)
@@ -299,6 +375,19 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
 #pragma unroll
     for (int s = 0; s < KMAX; ++s)
       if (s < k && ids[s] == e) g += gtl[s];
+    if (aux_w) {
+      if (!ar.pre_softmax) {
+#pragma unroll
+        for (int s = 0; s < KMAX; ++s)
+          if (s < k && aux_ids[s] == e) g += aux_sel[s];
+      } else {
+        float dp = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KMAX; ++s)
+          if (s < k && aux_ids[s] == e) dp += aux_dp[s];
+        g += expf(bf16_to_f32(logits[n * E + e]) - lse[n]) * (dp - aux_t);
+      }
+    }
     if (zc != 0.0f || ac != 0.0f) {
       const float l = bf16_to_f32(logits[n * E + e]);
       if (zc != 0.0f) g += zc * expf(l - lse[n]);
@@ -442,18 +531,19 @@ extern "C" int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, 
   return clear_error();
 }
 
-extern "C" int ffmoe_route_bwd(const void* go, const void* down, const int32_t* row_of,
-                               const int64_t* topk_idx, const float* topk_w, const void* logits,
-                               const float* lse, const int32_t* counts, const float* g_aux,
-                               const float* g_z, float aux_coeff, float z_coeff, int64_t N, int D,
-                               int E, int k, int gating, int capacity_mode, void* wgo,
-                               void* grad_logits, float* grad_w, void* stream) {
+static int route_bwd_impl(const void* go, const void* down, const int32_t* row_of,
+                          const int64_t* topk_idx, const float* topk_w, const void* logits,
+                          const float* lse, const int32_t* counts, const float* g_aux,
+                          const float* g_z, float aux_coeff, float z_coeff, int64_t N, int D, int E,
+                          int k, int gating, int capacity_mode, AuxRoute ar, void* wgo,
+                          void* grad_logits, float* grad_w, void* stream) {
   if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_route_bwd: D must be a positive multiple of 8");
   if (k < 1 || k > FFMOE_MAX_TOPK || E < 1 || E > FFMOE_MAX_EXPERTS)
     return set_error("ffmoe_route_bwd: bad k/E");
   if ((g_z != nullptr || gating == FFMOE_GATING_SIGMOID || g_aux != nullptr) && logits == nullptr)
     return set_error("ffmoe_route_bwd: logits required");
-  if (g_z != nullptr && lse == nullptr) return set_error("ffmoe_route_bwd: lse required");
+  if ((g_z != nullptr || (ar.through_weights && ar.pre_softmax)) && lse == nullptr)
+    return set_error("ffmoe_route_bwd: lse required");
   if (g_aux != nullptr && counts == nullptr) return set_error("ffmoe_route_bwd: counts required");
   const dim3 grid(static_cast<unsigned>((N + 3) / 4));
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -461,7 +551,7 @@ extern "C" int ffmoe_route_bwd(const void* go, const void* down, const int32_t* 
   hipLaunchKernelGGL(route_bwd_kernel<KM>, grid, dim3(256), 0, st,                              \
                      static_cast<const bf16_t*>(go), static_cast<const bf16_t*>(down), row_of,  \
                      topk_idx, topk_w, static_cast<const bf16_t*>(logits), lse, counts, g_aux,  \
-                     g_z, aux_coeff, z_coeff, N, D, E, k, gating, capacity_mode,                \
+                     g_z, aux_coeff, z_coeff, N, D, E, k, gating, capacity_mode, ar,            \
                      static_cast<bf16_t*>(wgo), static_cast<bf16_t*>(grad_logits), grad_w)
   if (k <= 2)
     FFMOE_RB(2);
@@ -474,6 +564,33 @@ extern "C" int ffmoe_route_bwd(const void* go, const void* down, const int32_t* 
 #undef FFMOE_RB
   if (check_launch("route_bwd_kernel")) return 1;
   return clear_error();
+}
+
+extern "C" int ffmoe_route_bwd(const void* go, const void* down, const int32_t* row_of,
+                               const int64_t* topk_idx, const float* topk_w, const void* logits,
+                               const float* lse, const int32_t* counts, const float* g_aux,
+                               const float* g_z, float aux_coeff, float z_coeff, int64_t N, int D,
+                               int E, int k, int gating, int capacity_mode, void* wgo,
+                               void* grad_logits, float* grad_w, void* stream) {
+  const AuxRoute ar{0, nullptr, nullptr, 0, 0.0f};
+  return route_bwd_impl(go, down, row_of, topk_idx, topk_w, logits, lse, counts, g_aux, g_z,
+                        aux_coeff, z_coeff, N, D, E, k, gating, capacity_mode, ar, wgo,
+                        grad_logits, grad_w, stream);
+}
+
+extern "C" int ffmoe_route_bwd_ex(const void* go, const void* down, const int32_t* row_of,
+                                  const int64_t* topk_idx, const float* topk_w, const void* logits,
+                                  const float* lse, const int32_t* counts, const float* g_aux,
+                                  const float* g_z, float aux_coeff, float z_coeff, int64_t N,
+                                  int D, int E, int k, int gating, int capacity_mode,
+                                  int aux_through_weights, const int64_t* aux_topk_idx,
+                                  const int32_t* aux_counts, int pre_softmax,
+                                  float scoring_factor, void* wgo, void* grad_logits,
+                                  float* grad_w, void* stream) {
+  const AuxRoute ar{aux_through_weights, aux_topk_idx, aux_counts, pre_softmax, scoring_factor};
+  return route_bwd_impl(go, down, row_of, topk_idx, topk_w, logits, lse, counts, g_aux, g_z,
+                        aux_coeff, z_coeff, N, D, E, k, gating, capacity_mode, ar, wgo,
+                        grad_logits, grad_w, stream);
 }
 
 extern "C" int ffmoe_glu_fwd(const void* up, int64_t M, int H, int activation, void* act,

@@ -37,6 +37,17 @@ static inline RouteWs route_ws(void* ws, int64_t N, int E) {
   return w;
 }
 
+// Routing options beyond the fast path (fused_moe.py:116-251).
+struct RouteOpts {
+  const float* bias;      // expert_bias [E] (selection only), or null
+  int bias_round;         // 1: logits + bias rounded to bf16 (a bf16 bias on bf16 logits)
+  int pre_softmax;        // softmax over all experts before selection
+  float scoring;          // > 0: weights scaled by scoring / top_k
+  int n_group;            // > 0: group-limited selection over n_group groups
+  int topk_group;         //   keeping the best topk_group groups
+  const bf16_t* noise;    // input jitter: logits from bf16(x * noise), or null
+};
+
 // Top-k insertion: keeps the KMAX best in (value desc, index asc) order, which
 // is the reference's k-round argmax with tie_break_left=True
 // (fused_topk.py:63-70).  An element displaced from slot s still precedes an
@@ -75,7 +86,7 @@ struct TopK {
 template <int ET, int KMAX, bool FROM_LOGITS>
 __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ gate,
-    const bf16_t* __restrict__ logits_in, const float* __restrict__ bias, int64_t N, int D,
+    const bf16_t* __restrict__ logits_in, RouteOpts o, int64_t N, int D,
     int E, int k, int gating, int need_ssum, bf16_t* __restrict__ logits_out,
     int64_t* __restrict__ topk_idx, float* __restrict__ topk_w, float* __restrict__ lse_out,
     int32_t* __restrict__ rank_local, RouteWs ws) {
@@ -122,6 +133,21 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
         const int kk = k0 + 32 * u + kq;
         av[u] = make_uint4(0, 0, 0, 0);
         if (row_ok && kk < D) av[u] = *reinterpret_cast<const uint4*>(xr + kk);
+      }
+      if (o.noise != nullptr) {  // input jitter: bf16(x * noise), as the reference's bf16 product
+        const bf16_t* nr = o.noise + (tok_base + (row_ok ? row : 0)) * static_cast<int64_t>(D);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int kk = k0 + 32 * u + kq;
+          if (row_ok && kk < D) {
+            float a[8], b[8];
+            unpack8(av[u], a);
+            unpack8(*reinterpret_cast<const uint4*>(nr + kk), b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] *= b[i];
+            av[u] = pack8(a);
+          }
+        }
       }
       if constexpr (ET <= 2) {
         uint4 bv[U][ET];
@@ -178,14 +204,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     float lse = 0.0f;
     if (t < ntok) {
       const bf16_t* lr = L + t * LS;
-      TopK<KMAX> tk;
-      tk.init();
+      // logsumexp of the logits (z-loss and the pre-softmax probabilities)
       float m = -INFINITY, s = 0.0f;
       for (int e = 0; e < E; ++e) {
         const float l = bf16_to_f32(lr[e]);
-        float sc = (gating == FFMOE_GATING_SOFTMAX) ? l : 1.0f / (1.0f + expf(-l));
-        if (bias != nullptr) sc += bias[e];
-        tk.push(sc, e, k);
         if (l > m) {
           s = s * expf(m - l) + 1.0f;
           m = l;
@@ -194,9 +216,65 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
         }
       }
       lse = m + logf(s);
+      float psum = 0.0f;  // pre-softmax: sum of exp(l - max) in expert order
+      if (o.pre_softmax)
+        for (int e = 0; e < E; ++e) psum += expf(bf16_to_f32(lr[e]) - m);
+      // selection score of expert e (fused_moe.py:144-200)
+      auto score = [&](int e) {
+        const float l = bf16_to_f32(lr[e]);
+        float sc;
+        if (gating == FFMOE_GATING_SOFTMAX)
+          sc = o.pre_softmax ? expf(l - m) / psum : l;
+        else
+          sc = 1.0f / (1.0f + expf(-l));
+        if (o.bias != nullptr) sc = o.bias_round ? round_bf16(sc + o.bias[e]) : sc + o.bias[e];
+        return sc;
+      };
+      TopK<KMAX> tk;
+      tk.init();
+      if (o.n_group > 0) {
+        // group-limited top-k (fused_moe.py:203-251): groups ranked by the sum
+        // of their best top_k/topk_group scores (or their best score), the
+        // best topk_group groups kept, top_k taken among their experts
+        const int epg = E / o.n_group;
+        const int per = k / o.topk_group;
+        // bf16 selection scores (softmax logits, unbiased or with a bf16 bias)
+        // are summed in fp32 and rounded to bf16, as torch sums a bf16 tensor
+        const bool bf16_scores = gating == FFMOE_GATING_SOFTMAX && !o.pre_softmax &&
+                                 (o.bias == nullptr || o.bias_round);
+        TopK<FFMOE_MAX_TOPK> tg;
+        tg.init();
+        for (int g = 0; g < o.n_group; ++g) {
+          float gs;
+          if (per > 1 && per <= epg) {
+            TopK<FFMOE_MAX_TOPK> tm;
+            tm.init();
+            for (int j = 0; j < epg; ++j) tm.push(score(g * epg + j), j, per);
+            gs = 0.0f;
+#pragma unroll
+            for (int q = 0; q < FFMOE_MAX_TOPK; ++q)
+              if (q < per) gs += tm.v[q];
+            if (bf16_scores) gs = round_bf16(gs);
+          } else {
+            gs = -INFINITY;
+            for (int j = 0; j < epg; ++j) gs = fmaxf(gs, score(g * epg + j));
+          }
+          tg.push(gs, g, o.topk_group);
+        }
+        uint32_t keep[FFMOE_MAX_EXPERTS / 32] = {0};
+#pragma unroll
+        for (int q = 0; q < FFMOE_MAX_TOPK; ++q)
+          if (q < o.topk_group) keep[tg.i[q] >> 5] |= 1u << (tg.i[q] & 31);
+        for (int e = 0; e < E; ++e) {
+          const int g = e / epg;
+          if (keep[g >> 5] >> (g & 31) & 1u) tk.push(score(e), e, k);
+        }
+      } else {
+        for (int e = 0; e < E; ++e) tk.push(score(e), e, k);
+      }
       float w[KMAX];
       float wsum = 0.0f;
-      if (gating == FFMOE_GATING_SOFTMAX) {
+      if (gating == FFMOE_GATING_SOFTMAX && !o.pre_softmax) {
         float mx = -INFINITY;
 #pragma unroll
         for (int q = 0; q < KMAX; ++q)
@@ -212,10 +290,12 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
         for (int q = 0; q < KMAX; ++q)
           if (q < k) w[q] = w[q] / wsum;
       } else {
+        // sigmoid scores, or pre-softmax probabilities, renormalised with +1e-6
 #pragma unroll
         for (int q = 0; q < KMAX; ++q) {
           if (q < k) {
-            w[q] = 1.0f / (1.0f + expf(-bf16_to_f32(lr[tk.i[q]])));
+            const float l = bf16_to_f32(lr[tk.i[q]]);
+            w[q] = (gating == FFMOE_GATING_SOFTMAX) ? expf(l - m) / psum : 1.0f / (1.0f + expf(-l));
             wsum += w[q];
           }
         }
@@ -223,6 +303,12 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
 #pragma unroll
         for (int q = 0; q < KMAX; ++q)
           if (q < k) w[q] = w[q] / wsum;
+      }
+      if (o.scoring > 0.0f) {
+        const float f = o.scoring / static_cast<float>(k);
+#pragma unroll
+        for (int q = 0; q < KMAX; ++q)
+          if (q < k) w[q] = w[q] * f;
       }
       const int64_t n = tok_base + t;
 #pragma unroll
@@ -417,33 +503,33 @@ __global__ __launch_bounds__(256) void permute_kernel(
 
 template <int ET, int KMAX, bool FL>
 static void launch_route(dim3 grid, size_t shm, hipStream_t st, const bf16_t* x, const bf16_t* gate,
-                         const bf16_t* li, const float* bias, int64_t N, int D, int E, int k,
+                         const bf16_t* li, const RouteOpts& o, int64_t N, int D, int E, int k,
                          int gating, int need_ssum, bf16_t* lo, int64_t* ti, float* tw, float* lse,
                          int32_t* rl, RouteWs ws) {
   hipLaunchKernelGGL((route_fwd_kernel<ET, KMAX, FL>), grid, dim3(kRouteThreads), shm, st, x, gate,
-                     li, bias, N, D, E, k, gating, need_ssum, lo, ti, tw, lse, rl, ws);
+                     li, o, N, D, E, k, gating, need_ssum, lo, ti, tw, lse, rl, ws);
 }
 
 template <int ET, int KMAX>
 static void launch_route_fl(bool fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
-                            const bf16_t* gate, const bf16_t* li, const float* bias, int64_t N,
+                            const bf16_t* gate, const bf16_t* li, const RouteOpts& o, int64_t N,
                             int D, int E, int k, int gating, int need_ssum, bf16_t* lo, int64_t* ti,
                             float* tw, float* lse, int32_t* rl, RouteWs ws) {
   if (fl)
-    launch_route<ET, KMAX, true>(grid, shm, st, x, gate, li, bias, N, D, E, k, gating, need_ssum,
+    launch_route<ET, KMAX, true>(grid, shm, st, x, gate, li, o, N, D, E, k, gating, need_ssum,
                                  lo, ti, tw, lse, rl, ws);
   else
-    launch_route<ET, KMAX, false>(grid, shm, st, x, gate, li, bias, N, D, E, k, gating, need_ssum,
+    launch_route<ET, KMAX, false>(grid, shm, st, x, gate, li, o, N, D, E, k, gating, need_ssum,
                                   lo, ti, tw, lse, rl, ws);
 }
 
 template <int ET>
 static void launch_route_k(int k, bool fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
-                           const bf16_t* gate, const bf16_t* li, const float* bias, int64_t N,
+                           const bf16_t* gate, const bf16_t* li, const RouteOpts& o, int64_t N,
                            int D, int E, int gating, int need_ssum, bf16_t* lo, int64_t* ti,
                            float* tw, float* lse, int32_t* rl, RouteWs ws) {
 #define FFMOE_RK(KM)                                                                           \
-  launch_route_fl<ET, KM>(fl, grid, shm, st, x, gate, li, bias, N, D, E, k, gating, need_ssum, \
+  launch_route_fl<ET, KM>(fl, grid, shm, st, x, gate, li, o, N, D, E, k, gating, need_ssum, \
                           lo, ti, tw, lse, rl, ws)
   if (k <= 2)
     FFMOE_RK(2);
@@ -471,11 +557,10 @@ extern "C" size_t ffmoe_route_workspace_bytes(int64_t N, int E, int k) {
   return rank_local_offset(N, E) + static_cast<size_t>(N) * k * 4;
 }
 
-extern "C" int ffmoe_route_fwd(const void* x, const void* gate, const void* logits_in,
-                               const float* expert_bias, int64_t N, int D, int E, int k,
-                               int gating, int need_sigmoid_sum, void* logits_out,
-                               int64_t* topk_idx, float* topk_w, float* lse, void* workspace,
-                               void* stream) {
+static int route_fwd_impl(const void* x, const void* gate, const void* logits_in, RouteOpts o,
+                          int64_t N, int D, int E, int k, int gating, int need_sigmoid_sum,
+                          void* logits_out, int64_t* topk_idx, float* topk_w, float* lse,
+                          void* workspace, void* stream) {
   if (N <= 0) return set_error("ffmoe_route_fwd: N must be positive");
   if (E < 1 || E > FFMOE_MAX_EXPERTS) return set_error("ffmoe_route_fwd: E out of range [1, 256]");
   if (k < 1 || k > E || k > FFMOE_MAX_TOPK)
@@ -486,6 +571,18 @@ extern "C" int ffmoe_route_fwd(const void* x, const void* gate, const void* logi
     return set_error("ffmoe_route_fwd: unknown gating");
   if (workspace == nullptr || topk_idx == nullptr || topk_w == nullptr)
     return set_error("ffmoe_route_fwd: null output");
+  if (o.n_group > 0) {
+    if (E % o.n_group != 0)
+      return set_error("ffmoe_route_fwd: E (" + std::to_string(E) + ") must be divisible by n_group (" +
+                       std::to_string(o.n_group) + ")");
+    if (o.topk_group < 1 || o.topk_group > o.n_group || o.topk_group > FFMOE_MAX_TOPK)
+      return set_error("ffmoe_route_fwd: topk_group must be in [1, min(n_group, 16)]");
+    if (o.topk_group * (E / o.n_group) < k)
+      return set_error("ffmoe_route_fwd: topk_group groups hold fewer than top_k experts");
+  }
+  if (o.noise != nullptr && logits_in != nullptr)
+    return set_error("ffmoe_route_fwd: input jitter needs the gate GEMM (no logits_in)");
+  if (gating != FFMOE_GATING_SOFTMAX) o.pre_softmax = 0;  // the reference ignores it there
   const int ET = E <= 16 ? 1 : E <= 32 ? 2 : E <= 64 ? 4 : E <= 128 ? 8 : 16;
   const int LS = ET * 16 + 2;  // bf16 elements per LDS logits row
   const size_t shm = static_cast<size_t>(kRouteTokens) * LS * 2 +
@@ -500,8 +597,8 @@ extern "C" int ffmoe_route_fwd(const void* x, const void* gate, const void* logi
   auto lb = static_cast<const bf16_t*>(logits_in);
   auto lo = static_cast<bf16_t*>(logits_out);
 #define FFMOE_RE(ETV)                                                                           \
-  launch_route_k<ETV>(k, fl, grid, shm, st, xb, gb, lb, expert_bias, N, D, E, gating,           \
-                      need_sigmoid_sum, lo, topk_idx, topk_w, lse, rl, ws)
+  launch_route_k<ETV>(k, fl, grid, shm, st, xb, gb, lb, o, N, D, E, gating, need_sigmoid_sum,   \
+                      lo, topk_idx, topk_w, lse, rl, ws)
   switch (ET) {
     case 1: FFMOE_RE(1); break;
     case 2: FFMOE_RE(2); break;
@@ -512,6 +609,29 @@ extern "C" int ffmoe_route_fwd(const void* x, const void* gate, const void* logi
 #undef FFMOE_RE
   if (check_launch("route_fwd_kernel")) return 1;
   return clear_error();
+}
+
+extern "C" int ffmoe_route_fwd(const void* x, const void* gate, const void* logits_in,
+                               const float* expert_bias, int64_t N, int D, int E, int k,
+                               int gating, int need_sigmoid_sum, void* logits_out,
+                               int64_t* topk_idx, float* topk_w, float* lse, void* workspace,
+                               void* stream) {
+  RouteOpts o{expert_bias, 0, 0, 0.0f, 0, 0, nullptr};
+  return route_fwd_impl(x, gate, logits_in, o, N, D, E, k, gating, need_sigmoid_sum, logits_out,
+                        topk_idx, topk_w, lse, workspace, stream);
+}
+
+extern "C" int ffmoe_route_fwd_ex(const void* x, const void* gate, const void* logits_in,
+                                  const float* expert_bias, int bias_round_bf16, int pre_softmax,
+                                  float scoring_factor, int n_group, int topk_group,
+                                  const void* jitter_noise, int64_t N, int D, int E, int k,
+                                  int gating, int need_sigmoid_sum, void* logits_out,
+                                  int64_t* topk_idx, float* topk_w, float* lse, void* workspace,
+                                  void* stream) {
+  RouteOpts o{expert_bias, bias_round_bf16, pre_softmax, scoring_factor, n_group, topk_group,
+              static_cast<const bf16_t*>(jitter_noise)};
+  return route_fwd_impl(x, gate, logits_in, o, N, D, E, k, gating, need_sigmoid_sum, logits_out,
+                        topk_idx, topk_w, lse, workspace, stream);
 }
 
 extern "C" int ffmoe_route_scan(int64_t N, int E, int k, int mt, int gemm_bm, float aux_coeff,

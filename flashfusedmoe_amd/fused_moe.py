@@ -97,9 +97,10 @@ class _FusedMoEFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, x, gate, w_up, w_down, expert_bias, cfg):
+    def forward(ctx, x, gate, w_up, w_down, expert_bias, cfg, rcfg):
         (top_k, activation, gating, capacity_factor, recompute, mt_user, allow_dropped,
          aux_coeff, z_coeff) = cfg
+        pre_softmax, scoring, n_group, topk_group, jitter, advanced = rcfg
         N, D = x.shape
         E = gate.shape[0]
         dtype = _compute_dtype(x.dtype)
@@ -122,13 +123,30 @@ class _FusedMoEFunction(torch.autograd.Function):
         gate_id = L.GATING[gating]
         act_id = L.ACTIVATION[activation]
         need_ssum = gating == "sigmoid" and aux_coeff > 0.0
+        # a bf16 bias is added to the bf16 logits in bf16 (fused_moe.py:176)
+        bias_round = (expert_bias is not None and expert_bias.dtype == torch.bfloat16
+                      and gating == "softmax" and not pre_softmax)
+        ropts = (bool(bias_round), bool(pre_softmax), float(scoring or 0.0), int(n_group or 0),
+                 int(topk_group or 0))
 
+        # routing of the losses block (and of dispatch, without jitter)
         (logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats, ws, aux,
          z) = ops.route(xc, gc, expert_bias, top_k, gate_id, mt, float(aux_coeff),
-                         float(z_coeff), need_ssum)
+                        float(z_coeff), need_ssum, *ropts)
+        aux_idx = aux_counts = None
+        istats_d = istats
+        if jitter > 0.0:
+            # dispatch routes bf16(x * noise) (fused_moe.py:329-332); the losses
+            # block, the metrics and the sigmoid / z / aux gradients keep the
+            # un-jittered logits (fused_moe.py:1165, :577-579)
+            noise = torch.empty_like(xc).uniform_(1.0 - jitter, 1.0 + jitter)
+            aux_idx, aux_counts = topk_idx, counts
+            (_, topk_idx, topk_w, _, counts, offsets, tile_offsets, _, istats_d, ws, _,
+             _) = ops.route(xc, gc, expert_bias, top_k, gate_id, mt, 0.0, 0.0, False, *ropts,
+                            noise)
 
         if not capacity_mode and not allow_dropped:
-            actual_max = int(istats[L.ISTAT_MAX].item())            # fused_moe.py:400-410
+            actual_max = int(istats_d[L.ISTAT_MAX].item())          # fused_moe.py:400-410
             if actual_max > mt:
                 raise RuntimeError(_overflow_message(actual_max, mt))
 
@@ -139,34 +157,44 @@ class _FusedMoEFunction(torch.autograd.Function):
             tw = topk_w
 
         ctx.cfg = (top_k, act_id, gate_id, capacity_mode, float(aux_coeff), float(z_coeff))
+        ctx.rcfg = (bool(advanced and gating == "softmax"), bool(pre_softmax),
+                    float(scoring or 0.0))
         ctx.in_dtypes = (x.dtype, gate.dtype, w_up.dtype, w_down.dtype)
         ctx.save_for_backward(xc, gc, wu, wd, logits, topk_idx, tw, lse, counts, offsets,
-                              tile_offsets, row_of, xs, up, act, down)
+                              tile_offsets, row_of, xs, up, act, down, aux_idx, aux_counts)
         ctx.set_materialize_grads(False)  # unused outputs get no zero-filled gradients
-        ctx.aux_has_grad = gating == "sigmoid"
-        non_diff = [topk_idx, counts, stats, istats]
+        # the softmax aux loss has a gradient only on the reference's slow
+        # routing path, whose weights are differentiable torch ops
+        # (fused_topk_routing outputs are not): fused_moe.py:136-142, :1165-1189
+        ctx.aux_has_grad = gating == "sigmoid" or bool(advanced)
+        # metrics come from the losses block's (un-jittered) routing
+        m_counts = aux_counts if aux_counts is not None else counts
+        non_diff = [m_counts, stats, istats]
         if not ctx.aux_has_grad:
-            # the reference's softmax aux loss has no gradient on its fused path
-            # (fused_topk_routing outputs are not differentiable)
             non_diff.append(aux)
         ctx.mark_non_differentiable(*non_diff)
-        return out, aux, z, topk_idx, counts, stats, istats
+        return out, aux, z, m_counts, stats, istats
 
     @staticmethod
-    def backward(ctx, grad_out, g_aux, g_z, _gi, _gc, _gs, _gis):
+    def backward(ctx, grad_out, g_aux, g_z, _gc, _gs, _gis):
         (xc, gc, wu, wd, logits, topk_idx, tw, lse, counts, offsets, tile_offsets, row_of, xs,
-         up, act, down) = ctx.saved_tensors
+         up, act, down, aux_idx, aux_counts) = ctx.saved_tensors
         top_k, act_id, gate_id, capacity_mode, aux_coeff, z_coeff = ctx.cfg
+        aux_through, pre_softmax, scoring = ctx.rcfg
         if grad_out is None:
             grad_out = torch.zeros_like(xc)
         go = grad_out.to(torch.bfloat16).contiguous()
         ga = g_aux if (ctx.aux_has_grad and aux_coeff > 0.0) else None
         gz = g_z if z_coeff > 0.0 else None
+        # the sigmoid aux gradient's expert fractions come from the losses
+        # block's routing (the un-jittered one under input jitter)
         dx, dgate, dwu, dwd = ops.experts_backward(
-            go, xc, gc, wu, wd, logits, topk_idx, tw, lse, counts, offsets, tile_offsets, row_of,
-            xs, up, act, down, ga, gz, top_k, act_id, gate_id, capacity_mode, aux_coeff, z_coeff)
+            go, xc, gc, wu, wd, logits, topk_idx, tw, lse,
+            counts if aux_counts is None else aux_counts, offsets, tile_offsets, row_of, xs, up,
+            act, down, ga, gz, top_k, act_id, gate_id, capacity_mode, aux_coeff, z_coeff,
+            aux_through, aux_idx, aux_counts, pre_softmax, scoring)
         xd, gd, ud, dd = ctx.in_dtypes
-        return dx.to(xd), dgate.to(gd), dwu.to(ud), dwd.to(dd), None, None
+        return dx.to(xd), dgate.to(gd), dwu.to(ud), dwd.to(dd), None, None, None
 
 
 def set_ep_group(group, backend="nccl"):
@@ -218,22 +246,31 @@ def fused_moe(
     if ep_group is not None:
         raise NotImplementedError("expert parallelism is not part of this single-GPU build")
     _validate_inputs(hidden_states, gate_weight, w_up, w_down, top_k, activation, gating)
-    if n_group is not None or topk_group is not None or pre_softmax or scoring_factor is not None:
-        raise NotImplementedError("group-limited / pre-softmax / scoring-factor routing is "
-                                  "not implemented yet")
-    if input_jitter > 0.0 and hidden_states.requires_grad:
-        raise NotImplementedError("input_jitter is not implemented yet")
 
     N, D = hidden_states.shape
     E = gate_weight.shape[0]
     H = w_up.shape[1] // 2
     _check_kernel_limits(N, D, E, H, top_k)
+    # the reference's slow routing path (fused_moe.py:136-138)
+    advanced = (n_group is not None or expert_bias is not None or pre_softmax
+                or scoring_factor is not None)
+    groups = n_group is not None and topk_group is not None          # fused_moe.py:158, :175
+    if groups:
+        assert E % n_group == 0, f"E ({E}) must be divisible by n_group ({n_group})"  # :225
+        if not 1 <= topk_group <= min(n_group, L.MAX_TOPK):
+            raise NotImplementedError(f"ffmoe kernels need 1 <= topk_group <= min(n_group, "
+                                      f"{L.MAX_TOPK}), got {topk_group}")
+        if topk_group * (E // n_group) < top_k:
+            raise NotImplementedError("the selected groups must hold at least top_k experts")
+    jitter = float(input_jitter) if (input_jitter > 0.0 and hidden_states.requires_grad) else 0.0
 
     cfg = (top_k, activation, gating, capacity_factor, bool(recompute_activations),
            max_tokens_per_expert, bool(allow_dropped_tokens), float(aux_loss_coeff),
            float(z_loss_coeff))
-    out, aux, z, topk_idx, counts, stats, istats = _FusedMoEFunction.apply(
-        hidden_states, gate_weight, w_up, w_down, expert_bias, cfg)
+    rcfg = (bool(pre_softmax), scoring_factor, n_group if groups else None,
+            topk_group if groups else None, jitter, bool(advanced))
+    out, aux, z, counts, stats, istats = _FusedMoEFunction.apply(
+        hidden_states, gate_weight, w_up, w_down, expert_bias, cfg, rcfg)
 
     losses = {}
     if aux_loss_coeff > 0.0:

@@ -38,12 +38,15 @@ def _check_bf16_gpu(name, t):
 
 @torch.library.custom_op("ffmoe::route", mutates_args=())
 def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, gating: int,
-          mt: int, aux_coeff: float, z_coeff: float, need_ssum: bool) -> List[Tensor]:
+          mt: int, aux_coeff: float, z_coeff: float, need_ssum: bool, bias_round: bool = False,
+          pre_softmax: bool = False, scoring: float = 0.0, n_group: int = 0, topk_group: int = 0,
+          noise: Optional[Tensor] = None) -> List[Tensor]:
     """Returns [logits bf16 [N,E], topk_idx int64 [N,k], topk_w fp32 [N,k],
     lse fp32 [N], counts int32 [E], offsets int32 [E+1], tile_offsets int32
     [E+1], stats fp32 [4], istats int32 [4], workspace uint8, aux_loss fp32 [],
     z_loss fp32 []] (the two losses repeat stats[AUX] and stats[Z] as
-    separate tensors)."""
+    separate tensors).  bias_round / pre_softmax / scoring / n_group /
+    topk_group / noise are ffmoe_route_fwd_ex's routing options."""
     _check_bf16_gpu("hidden_states", x)
     _check_bf16_gpu("gate_weight", gate)
     N, D = x.shape
@@ -66,8 +69,12 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
     if expert_bias is not None:
         bias = expert_bias.to(device=dev, dtype=torch.float32).contiguous()
     st = L.stream_ptr(dev)
-    L.call("ffmoe_route_fwd", L.ptr(x), L.ptr(gate), None, L.ptr(bias), N, D, E, k, gating,
-           int(need_ssum), L.ptr(logits), L.ptr(topk_idx), L.ptr(topk_w), L.ptr(lse), L.ptr(ws), st)
+    if noise is not None:
+        _check_bf16_gpu("input jitter noise", noise)
+    L.call("ffmoe_route_fwd_ex", L.ptr(x), L.ptr(gate), None, L.ptr(bias), int(bias_round),
+           int(pre_softmax), float(scoring), int(n_group), int(topk_group), L.ptr(noise), N, D, E,
+           k, gating, int(need_ssum), L.ptr(logits), L.ptr(topk_idx), L.ptr(topk_w), L.ptr(lse),
+           L.ptr(ws), st)
     L.call("ffmoe_route_scan", N, E, k, mt, L.gemm_tile_rows(N * k, E), aux_coeff, z_coeff, gating,
            L.ptr(ws), L.ptr(counts), L.ptr(offsets), L.ptr(tile_offsets), L.ptr(stats),
            L.ptr(istats), L.ptr(aux), L.ptr(z), st)
@@ -75,7 +82,9 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
 
 
 @route.register_fake
-def _route_fake(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, need_ssum):
+def _route_fake(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, need_ssum,
+                bias_round=False, pre_softmax=False, scoring=0.0, n_group=0, topk_group=0,
+                noise=None):
     N, D = x.shape
     E = gate.shape[0]
     f = lambda *s, dtype: x.new_empty(s, dtype=dtype)  # noqa: E731
@@ -165,9 +174,13 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
                      offsets: Tensor, tile_offsets: Tensor, row_of: Tensor, xs: Tensor, up: Tensor,
                      act: Tensor, down: Tensor, g_aux: Optional[Tensor], g_z: Optional[Tensor],
                      top_k: int, activation: int, gating: int, capacity_mode: bool,
-                     aux_coeff: float, z_coeff: float) -> List[Tensor]:
+                     aux_coeff: float, z_coeff: float, aux_through_weights: bool = False,
+                     aux_idx: Optional[Tensor] = None, aux_counts: Optional[Tensor] = None,
+                     pre_softmax: bool = False, scoring: float = 0.0) -> List[Tensor]:
     """Returns [grad_hidden [N,D], grad_gate [E,D], grad_w_up [E,2H,D],
-    grad_w_down [E,D,H]], all bf16.  Empty up/act/down trigger recompute."""
+    grad_w_down [E,D,H]], all bf16.  Empty up/act/down trigger recompute.
+    logits / lse are the un-jittered ones; aux_* describe the aux loss's own
+    routing (ffmoe_route_bwd_ex)."""
     _check_bf16_gpu("grad_output", go)
     N, D = x.shape
     E, H2, _ = w_up.shape
@@ -182,10 +195,11 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     gl = torch.empty(N, E, dtype=_BF16, device=dev)
     ga = None if g_aux is None else g_aux.to(device=dev, dtype=torch.float32).contiguous()
     gz = None if g_z is None else g_z.to(device=dev, dtype=torch.float32).contiguous()
-    L.call("ffmoe_route_bwd", L.ptr(go), L.ptr(down), L.ptr(row_of), L.ptr(topk_idx),
+    L.call("ffmoe_route_bwd_ex", L.ptr(go), L.ptr(down), L.ptr(row_of), L.ptr(topk_idx),
            L.ptr(topk_w), L.ptr(logits), L.ptr(lse), L.ptr(counts), L.ptr(ga), L.ptr(gz),
-           aux_coeff, z_coeff, N, D, E, k, gating, int(capacity_mode), L.ptr(wgo), L.ptr(gl),
-           None, st)
+           aux_coeff, z_coeff, N, D, E, k, gating, int(capacity_mode), int(aux_through_weights),
+           L.ptr(aux_idx), L.ptr(aux_counts), int(pre_softmax), float(scoring), L.ptr(wgo),
+           L.ptr(gl), None, st)
     gup = torch.empty(T, H2, dtype=_BF16, device=dev)
     tr = L.gemm_tile_rows(T, E)
     ws = L.ptr(L.gemm_workspace(dev, st))

@@ -106,6 +106,26 @@ int ffmoe_route_fwd(const void* x, const void* gate, const void* logits_in,
                     int64_t* topk_idx, float* topk_w, float* lse,
                     void* workspace, void* stream);
 
+/* ffmoe_route_fwd with the routing options of the reference's slow path
+ * (`_apply_routing`, fused_moe.py:116-200, and `_group_limited_topk`
+ * :203-251, with the input jitter of :329-332):
+ *   expert_bias      [E] fp32, added to the selection scores only;
+ *   bias_round_bf16  1 when the caller's bias is bf16 (softmax gating without
+ *                    pre_softmax adds it to the bf16 logits in bf16);
+ *   pre_softmax      softmax over all experts before selection, weights the
+ *                    selected probabilities renormalised (+1e-6);
+ *   scoring_factor   > 0: weights scaled by scoring_factor / k;
+ *   n_group, topk_group  > 0: group-limited selection (E % n_group == 0);
+ *   jitter_noise     [N,D] bf16 or NULL: logits from bf16(x * noise).
+ * Selection ties go to the lower index (groups and experts). */
+int ffmoe_route_fwd_ex(const void* x, const void* gate, const void* logits_in,
+                       const float* expert_bias, int bias_round_bf16,
+                       int pre_softmax, float scoring_factor, int n_group,
+                       int topk_group, const void* jitter_noise, int64_t N, int D,
+                       int E, int k, int gating, int need_sigmoid_sum,
+                       void* logits_out, int64_t* topk_idx, float* topk_w,
+                       float* lse, void* workspace, void* stream);
+
 /* Global prefix over the per-block expert histograms, losses and metrics.
  * Replaces: `bincount`/`cumsum` (fused_moe.py:346-348), the overflow check's
  *   max (fused_moe.py:401), the aux/z-loss and metrics reductions
@@ -254,6 +274,23 @@ int ffmoe_route_bwd(const void* go, const void* down, const int32_t* row_of,
                     float z_coeff, int64_t N, int D, int E, int k, int gating,
                     int capacity_mode, void* wgo, void* grad_logits,
                     float* grad_w, void* stream);
+
+/* ffmoe_route_bwd plus the aux-loss gradient through the routing weights,
+ * which the reference's slow routing path makes differentiable (softmax
+ * gating with expert_bias, pre_softmax, scoring_factor or n_group:
+ * fused_moe.py:144-200, :1165-1189).  aux_topk_idx / aux_counts: the aux
+ * loss's own routing (it differs from the dispatch routing under input
+ * jitter) or NULL for the dispatch routing; logits and lse must then be the
+ * un-jittered ones.  pre_softmax / scoring_factor as in ffmoe_route_fwd_ex. */
+int ffmoe_route_bwd_ex(const void* go, const void* down, const int32_t* row_of,
+                       const int64_t* topk_idx, const float* topk_w,
+                       const void* logits, const float* lse, const int32_t* counts,
+                       const float* g_aux, const float* g_z, float aux_coeff,
+                       float z_coeff, int64_t N, int D, int E, int k, int gating,
+                       int capacity_mode, int aux_through_weights,
+                       const int64_t* aux_topk_idx, const int32_t* aux_counts,
+                       int pre_softmax, float scoring_factor, void* wgo,
+                       void* grad_logits, float* grad_w, void* stream);
 
 /* Standalone GLU kernels (the reference's `activation_forward` /
  * `activation_backward`, activations.py:145-231).  up [M, 2H] bf16 ->

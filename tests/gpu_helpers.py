@@ -34,6 +34,17 @@ def check_close(actual, expected, name, rtol=RTOL, atol=ATOL, max_bad_frac=1e-3)
     return rel_l2
 
 
+def check_as_accurate(actual, oracle_bf16, exact, name, slack=1.25):
+    """The HIP result is at least about as close to an fp64 restatement as
+    the bf16 oracle is: relative L2 error against ``exact`` within ``slack``
+    times the oracle's own."""
+    a, o, t = (v.detach().double().cpu() for v in (actual, oracle_bf16, exact))
+    ea = ((a - t).norm() / t.norm()).item()
+    eo = ((o - t).norm() / t.norm()).item()
+    assert ea <= slack * eo + 1e-7, f"{name}: error vs fp64 {ea:.3e} > {slack} x oracle's {eo:.3e}"
+    return ea, eo
+
+
 def seeded(N, D, ffn, E, seed=0, gate_scale=None, w_scale=None, dtype=torch.bfloat16):
     """Inputs generated on the CPU in fp32 then cast: CPU oracle and GPU see
     identical bits.  Default weights ~ N(0, 1/fan_in)."""
