@@ -256,7 +256,7 @@ def fused_moe(
                 or scoring_factor is not None)
     groups = n_group is not None and topk_group is not None          # fused_moe.py:158, :175
     if groups:
-        assert E % n_group == 0, f"E ({E}) must be divisible by n_group ({n_group})"  # :225
+        assert E % n_group == 0, f"E ({E}) must be divisible by n_group ({n_group})"  # fused_moe.py:221
         if not 1 <= topk_group <= min(n_group, L.MAX_TOPK):
             raise NotImplementedError(f"ffmoe kernels need 1 <= topk_group <= min(n_group, "
                                       f"{L.MAX_TOPK}), got {topk_group}")
