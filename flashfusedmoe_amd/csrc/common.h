@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 #include <string>
@@ -78,11 +79,14 @@ __device__ __forceinline__ float fast_sigmoid(float x) {
 
 // GLU activations in fp32 (the reference computes them in fp32 from bf16
 // operands, activations.py:27-142).  tanh is taken as 2*sigmoid(2z) - 1
-// (activations.py:21-24).
-__device__ __forceinline__ float glu_fwd(int act, float g, float u) {
-  if (act == FFMOE_ACT_SWIGLU) {
+// (activations.py:21-24).  The activation is a template argument so that
+// hot loops carry no per-element branch; with_act() dispatches a runtime
+// activation id once.
+template <int ACT>
+__device__ __forceinline__ float glu_fwd_t(float g, float u) {
+  if constexpr (ACT == FFMOE_ACT_SWIGLU) {
     return g * fast_sigmoid(g) * u;
-  } else if (act == FFMOE_ACT_GEGLU) {
+  } else if constexpr (ACT == FFMOE_ACT_GEGLU) {
     const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
     const float th = 2.0f * fast_sigmoid(2.0f * inner) - 1.0f;
     return 0.5f * g * (1.0f + th) * u;
@@ -93,13 +97,13 @@ __device__ __forceinline__ float glu_fwd(int act, float g, float u) {
 }
 
 // d(act)/d(gate), d(act)/d(up) scaled by the upstream grad `ga`.
-__device__ __forceinline__ void glu_bwd(int act, float ga, float g, float u, float* gg,
-                                        float* gu) {
-  if (act == FFMOE_ACT_SWIGLU) {
+template <int ACT>
+__device__ __forceinline__ void glu_bwd_t(float ga, float g, float u, float* gg, float* gu) {
+  if constexpr (ACT == FFMOE_ACT_SWIGLU) {
     const float s = fast_sigmoid(g);
     *gu = ga * g * s;
     *gg = ga * u * (s * (1.0f + g * (1.0f - s)));
-  } else if (act == FFMOE_ACT_GEGLU) {
+  } else if constexpr (ACT == FFMOE_ACT_GEGLU) {
     const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
     const float th = 2.0f * fast_sigmoid(2.0f * inner) - 1.0f;
     const float gelu = 0.5f * g * (1.0f + th);
@@ -112,6 +116,27 @@ __device__ __forceinline__ void glu_bwd(int act, float ga, float g, float u, flo
     *gu = ga * r * r;
     *gg = ga * u * 2.0f * r;
   }
+}
+
+// Calls f(std::integral_constant<int, ACT>) for a runtime activation id.
+template <class F>
+__device__ __forceinline__ void with_act(int act, F&& f) {
+  if (act == FFMOE_ACT_SWIGLU)
+    f(std::integral_constant<int, FFMOE_ACT_SWIGLU>{});
+  else if (act == FFMOE_ACT_GEGLU)
+    f(std::integral_constant<int, FFMOE_ACT_GEGLU>{});
+  else
+    f(std::integral_constant<int, FFMOE_ACT_RELU2>{});
+}
+
+__device__ __forceinline__ float glu_fwd(int act, float g, float u) {
+  float r = 0.0f;
+  with_act(act, [&](auto a) { r = glu_fwd_t<decltype(a)::value>(g, u); });
+  return r;
+}
+
+__device__ __forceinline__ void glu_bwd(int act, float ga, float g, float u, float* gg, float* gu) {
+  with_act(act, [&](auto a) { glu_bwd_t<decltype(a)::value>(ga, g, u, gg, gu); });
 }
 
 }  // namespace ffmoe

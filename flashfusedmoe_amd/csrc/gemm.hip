@@ -141,6 +141,65 @@ __device__ __forceinline__ bf16x8_t lds_frag_mn_sw(const bf16_t* t, int c0, int 
   return bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// GLU backward epilogue, split in two so the pre-activation loads can be in
+// flight while the accumulators are staged: item i of a thread covers row
+// row_base + idx / (BN/8) and columns n0 + (idx % (BN/8))*8 .. +8 of the
+// tile, idx = i * kThreads + tid.  All loads are issued before any store (a
+// vector-memory wait would also drain earlier stores).
+template <int ROWS, int BN>
+constexpr int glu_bwd_items() { return ROWS * (BN / 8) / kThreads; }
+
+template <int ROWS, int BN>
+__device__ __forceinline__ void glu_bwd_prefetch(const GemmArgs& p, int row_base, int row_end, int n0,
+                                                 uint4* pg, uint4* pu) {
+  constexpr int CH = BN / 8;
+  constexpr int IT = glu_bwd_items<ROWS, BN>();
+  static_assert((ROWS * CH) % kThreads == 0, "whole items");
+  const int tid = threadIdx.x;
+  const int64_t H = p.H;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int idx = it * kThreads + tid;
+    const int64_t row = static_cast<int64_t>(row_base) + idx / CH;
+    const int col = n0 + (idx % CH) * 8;
+    pg[it] = make_uint4(0, 0, 0, 0);
+    pu[it] = make_uint4(0, 0, 0, 0);
+    if (row < row_end && col < p.N) {
+      pg[it] = *reinterpret_cast<const uint4*>(p.up + row * 2 * H + col);
+      pu[it] = *reinterpret_cast<const uint4*>(p.up + row * 2 * H + H + col);
+    }
+  }
+}
+
+template <int ROWS, int BN, int LDC>
+__device__ __forceinline__ void glu_bwd_store(const GemmArgs& p, const bf16_t* Cs, int row_base, int row_end,
+                                              int n0, const uint4* pg, const uint4* pu) {
+  constexpr int CH = BN / 8;
+  constexpr int IT = glu_bwd_items<ROWS, BN>();
+  const int tid = threadIdx.x;
+  const int64_t H = p.H;
+  with_act(p.act, [&](auto actc) {
+    constexpr int ACT = decltype(actc)::value;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int idx = it * kThreads + tid;
+      const int ml = idx / CH, c = (idx % CH) * 8;
+      const int64_t row = static_cast<int64_t>(row_base) + ml;
+      const int col = n0 + c;
+      if (row < row_end && col < p.N) {
+        float ga[8], g[8], u[8], gg[8], gu[8];
+        unpack8(*reinterpret_cast<const uint4*>(Cs + ml * LDC + c), ga);
+        unpack8(pg[it], g);
+        unpack8(pu[it], u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) glu_bwd_t<ACT>(ga[i], g[i], u[i], &gg[i], &gu[i]);
+        *reinterpret_cast<uint4*>(p.C + row * 2 * H + col) = pack8(gg);
+        *reinterpret_cast<uint4*>(p.C + row * 2 * H + H + col) = pack8(gu);
+      }
+    }
+  });
+}
+
 // Stores ROWS rows of a bf16 C tile staged in LDS (row stride LDC) with the
 // block's 256 threads, 16 bytes each: plain store, GLU forward (tile columns
 // [0, BN/2) gate, [BN/2, BN) up: writes act and, if requested, the
@@ -153,64 +212,37 @@ __device__ __forceinline__ void store_c_tile(const GemmArgs& p, const bf16_t* Cs
   const int tid = threadIdx.x;
   if constexpr (EPI == EPI_GLU_FWD) {
     constexpr int CH = BN / 16;  // 8-column chunks per half row
+    constexpr int IT = ROWS * CH / kThreads;
+    static_assert((ROWS * CH) % kThreads == 0, "whole items");
     const int64_t H = p.H;
-    for (int idx = tid; idx < ROWS * CH; idx += kThreads) {
-      const int ml = idx / CH, c = (idx % CH) * 8;
-      const int64_t row = row_base + ml;
-      const int a = a0 + c;
-      if (row >= row_end || a >= p.H) continue;
-      const uint4 gv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
-      const uint4 uv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + BN / 2 + c);
-      float g[8], u[8], o[8];
-      unpack8(gv, g);
-      unpack8(uv, u);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = glu_fwd(p.act, g[i], u[i]);
-      if (p.C2 != nullptr) {
-        *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + a) = gv;
-        *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + H + a) = uv;
-      }
-      *reinterpret_cast<uint4*>(p.C + row * p.ldc + a) = pack8(o);
-    }
-  } else if constexpr (EPI == EPI_GLU_BWD) {
-    // batches of NB chunks: all pre-activation loads of a batch are issued
-    // before any of its stores (a vector-memory wait also drains earlier
-    // stores, so interleaving loads and stores would serialise them)
-    constexpr int CH = BN / 8;
-    constexpr int NB = 4;
-    static_assert((ROWS * CH) % (kThreads * NB) == 0, "whole batches");
-    const int64_t H = p.H;
-    for (int base = 0; base < ROWS * CH; base += kThreads * NB) {
-      uint4 gv[NB], uv[NB], cv[NB];
-      int64_t rowv[NB];
-      int colv[NB];
-      bool ok[NB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const int idx = base + b * kThreads + tid;
+    with_act(p.act, [&](auto actc) {
+      constexpr int ACT = decltype(actc)::value;
+#pragma unroll 4
+      for (int it = 0; it < IT; ++it) {
+        const int idx = it * kThreads + tid;
         const int ml = idx / CH, c = (idx % CH) * 8;
-        rowv[b] = static_cast<int64_t>(row_base) + ml;
-        colv[b] = n0 + c;
-        ok[b] = rowv[b] < row_end && colv[b] < p.N;
-        cv[b] = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
-        if (ok[b]) {
-          gv[b] = *reinterpret_cast<const uint4*>(p.up + rowv[b] * 2 * H + colv[b]);
-          uv[b] = *reinterpret_cast<const uint4*>(p.up + rowv[b] * 2 * H + H + colv[b]);
+        const int64_t row = row_base + ml;
+        const int a = a0 + c;
+        if (row < row_end && a < p.H) {
+          const uint4 gv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
+          const uint4 uv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + BN / 2 + c);
+          float g[8], u[8], o[8];
+          unpack8(gv, g);
+          unpack8(uv, u);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = glu_fwd_t<ACT>(g[i], u[i]);
+          if (p.C2 != nullptr) {
+            *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + a) = gv;
+            *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + H + a) = uv;
+          }
+          *reinterpret_cast<uint4*>(p.C + row * p.ldc + a) = pack8(o);
         }
       }
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        if (!ok[b]) continue;
-        float ga[8], g[8], u[8], gg[8], gu[8];
-        unpack8(cv[b], ga);
-        unpack8(gv[b], g);
-        unpack8(uv[b], u);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) glu_bwd(p.act, ga[i], g[i], u[i], &gg[i], &gu[i]);
-        *reinterpret_cast<uint4*>(p.C + rowv[b] * 2 * H + colv[b]) = pack8(gg);
-        *reinterpret_cast<uint4*>(p.C + rowv[b] * 2 * H + H + colv[b]) = pack8(gu);
-      }
-    }
+    });
+  } else if constexpr (EPI == EPI_GLU_BWD) {
+    uint4 pg[glu_bwd_items<ROWS, BN>()], pu[glu_bwd_items<ROWS, BN>()];
+    glu_bwd_prefetch<ROWS, BN>(p, row_base, row_end, n0, pg, pu);
+    glu_bwd_store<ROWS, BN, LDC>(p, Cs, row_base, row_end, n0, pg, pu);
   } else {
     constexpr int CH = BN / 8;
     bf16_t* Cb = p.C;
@@ -221,20 +253,7 @@ __device__ __forceinline__ void store_c_tile(const GemmArgs& p, const bf16_t* Cs
       const bool row_ok = (MODE == 0) ? row < row_end : row < p.M;
       const int col = n0 + c;
       if (!row_ok || col >= p.N) continue;
-      const uint4 cv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
-      if constexpr (EPI == EPI_GLU_BWD) {
-        const int64_t H = p.H;
-        float ga[8], g[8], u[8], gg[8], gu[8];
-        unpack8(cv, ga);
-        unpack8(*reinterpret_cast<const uint4*>(p.up + row * 2 * H + col), g);
-        unpack8(*reinterpret_cast<const uint4*>(p.up + row * 2 * H + H + col), u);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) glu_bwd(p.act, ga[i], g[i], u[i], &gg[i], &gu[i]);
-        *reinterpret_cast<uint4*>(Cb + row * 2 * H + col) = pack8(gg);
-        *reinterpret_cast<uint4*>(Cb + row * 2 * H + H + col) = pack8(gu);
-      } else {
-        *reinterpret_cast<uint4*>(Cb + row * p.ldc + col) = cv;
-      }
+      *reinterpret_cast<uint4*>(Cb + row * p.ldc + col) = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
     }
   }
 }
@@ -888,10 +907,17 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
       }
     }
   };
+  // the GLU backward's pre-activation loads fly while the tile is staged
+  constexpr int PIT = (EPI == EPI_GLU_BWD) ? glu_bwd_items<BM, BN>() : 1;
+  uint4 pre_g[PIT], pre_u[PIT];
+  if constexpr (EPI == EPI_GLU_BWD) glu_bwd_prefetch<BM, BN>(p, row_begin, row_end, n0, pre_g, pre_u);
   if (role == ROLE_OWNER) stage(std::true_type{});
   else stage(std::false_type{});
   __syncthreads();
-  store_c_tile<BM, BN, LDC, MODE, EPI>(p, Cs, e, m0, row_begin, row_end, n0, a0);
+  if constexpr (EPI == EPI_GLU_BWD)
+    glu_bwd_store<BM, BN, LDC>(p, Cs, row_begin, row_end, n0, pre_g, pre_u);
+  else
+    store_c_tile<BM, BN, LDC, MODE, EPI>(p, Cs, e, m0, row_begin, row_end, n0, a0);
   __syncthreads();  // the C tile is read before a next tile's loads refill the LDS
 }
 
