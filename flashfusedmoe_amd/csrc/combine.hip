@@ -400,8 +400,9 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
   }
 }
 
+template <int ACT>
 __global__ __launch_bounds__(256) void glu_fwd_kernel(const bf16_t* __restrict__ up, int64_t M,
-                                                      int H, int act, bf16_t* __restrict__ out) {
+                                                      int H, bf16_t* __restrict__ out) {
   const int hv = H / 8;
   const int64_t total = M * hv;
   for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
@@ -412,14 +413,15 @@ __global__ __launch_bounds__(256) void glu_fwd_kernel(const bf16_t* __restrict__
     unpack8(reinterpret_cast<const uint4*>(up + m * 2 * H)[v], g);
     unpack8(reinterpret_cast<const uint4*>(up + m * 2 * H + H)[v], x);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = glu_fwd(act, g[i], x[i]);
+    for (int i = 0; i < 8; ++i) o[i] = glu_fwd_t<ACT>(g[i], x[i]);
     reinterpret_cast<uint4*>(out + m * H)[v] = pack8(o);
   }
 }
 
+template <int ACT>
 __global__ __launch_bounds__(256) void glu_bwd_kernel(const bf16_t* __restrict__ ga,
                                                       const bf16_t* __restrict__ up, int64_t M,
-                                                      int H, int act, bf16_t* __restrict__ gup) {
+                                                      int H, bf16_t* __restrict__ gup) {
   const int hv = H / 8;
   const int64_t total = M * hv;
   for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
@@ -431,7 +433,7 @@ __global__ __launch_bounds__(256) void glu_bwd_kernel(const bf16_t* __restrict__
     unpack8(reinterpret_cast<const uint4*>(up + m * 2 * H)[v], g);
     unpack8(reinterpret_cast<const uint4*>(up + m * 2 * H + H)[v], x);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) glu_bwd(act, a[i], g[i], x[i], &og[i], &ou[i]);
+    for (int i = 0; i < 8; ++i) glu_bwd_t<ACT>(a[i], g[i], x[i], &og[i], &ou[i]);
     reinterpret_cast<uint4*>(gup + m * 2 * H)[v] = pack8(og);
     reinterpret_cast<uint4*>(gup + m * 2 * H + H)[v] = pack8(ou);
   }
@@ -596,11 +598,18 @@ extern "C" int ffmoe_route_bwd_ex(const void* go, const void* down, const int32_
 extern "C" int ffmoe_glu_fwd(const void* up, int64_t M, int H, int activation, void* act,
                              void* stream) {
   if (M < 0 || H <= 0 || H % 8 != 0) return set_error("ffmoe_glu_fwd: H must be a positive multiple of 8");
-  if (activation < 0 || activation > 2) return set_error("ffmoe_glu_fwd: unknown activation");
+  if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_glu_fwd: unknown activation");
   if (M == 0) return clear_error();
-  hipLaunchKernelGGL(glu_fwd_kernel, dim3(grid_for(M * (H / 8))), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(up), M, H,
-                     activation, static_cast<bf16_t*>(act));
+  const dim3 grid(grid_for(M * (H / 8)));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bf16_t* u = static_cast<const bf16_t*>(up);
+  bf16_t* o = static_cast<bf16_t*>(act);
+  switch (activation) {
+    case FFMOE_ACT_SWIGLU: hipLaunchKernelGGL(glu_fwd_kernel<FFMOE_ACT_SWIGLU>, grid, dim3(256), 0, st, u, M, H, o); break;
+    case FFMOE_ACT_GEGLU: hipLaunchKernelGGL(glu_fwd_kernel<FFMOE_ACT_GEGLU>, grid, dim3(256), 0, st, u, M, H, o); break;
+    case FFMOE_ACT_RELU2: hipLaunchKernelGGL(glu_fwd_kernel<FFMOE_ACT_RELU2>, grid, dim3(256), 0, st, u, M, H, o); break;
+    default: hipLaunchKernelGGL(glu_fwd_kernel<FFMOE_ACT_GEGLU_ERF>, grid, dim3(256), 0, st, u, M, H, o); break;
+  }
   if (check_launch("glu_fwd_kernel")) return 1;
   return clear_error();
 }
@@ -608,11 +617,19 @@ extern "C" int ffmoe_glu_fwd(const void* up, int64_t M, int H, int activation, v
 extern "C" int ffmoe_glu_bwd(const void* grad_act, const void* up, int64_t M, int H, int activation,
                              void* grad_up, void* stream) {
   if (M < 0 || H <= 0 || H % 8 != 0) return set_error("ffmoe_glu_bwd: H must be a positive multiple of 8");
-  if (activation < 0 || activation > 2) return set_error("ffmoe_glu_bwd: unknown activation");
+  if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_glu_bwd: unknown activation");
   if (M == 0) return clear_error();
-  hipLaunchKernelGGL(glu_bwd_kernel, dim3(grid_for(M * (H / 8))), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(grad_act),
-                     static_cast<const bf16_t*>(up), M, H, activation, static_cast<bf16_t*>(grad_up));
+  const dim3 grid(grid_for(M * (H / 8)));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bf16_t* ga = static_cast<const bf16_t*>(grad_act);
+  const bf16_t* u = static_cast<const bf16_t*>(up);
+  bf16_t* o = static_cast<bf16_t*>(grad_up);
+  switch (activation) {
+    case FFMOE_ACT_SWIGLU: hipLaunchKernelGGL(glu_bwd_kernel<FFMOE_ACT_SWIGLU>, grid, dim3(256), 0, st, ga, u, M, H, o); break;
+    case FFMOE_ACT_GEGLU: hipLaunchKernelGGL(glu_bwd_kernel<FFMOE_ACT_GEGLU>, grid, dim3(256), 0, st, ga, u, M, H, o); break;
+    case FFMOE_ACT_RELU2: hipLaunchKernelGGL(glu_bwd_kernel<FFMOE_ACT_RELU2>, grid, dim3(256), 0, st, ga, u, M, H, o); break;
+    default: hipLaunchKernelGGL(glu_bwd_kernel<FFMOE_ACT_GEGLU_ERF>, grid, dim3(256), 0, st, ga, u, M, H, o); break;
+  }
   if (check_launch("glu_bwd_kernel")) return 1;
   return clear_error();
 }

@@ -90,6 +90,8 @@ __device__ __forceinline__ float glu_fwd_t(float g, float u) {
     const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
     const float th = 2.0f * fast_sigmoid(2.0f * inner) - 1.0f;
     return 0.5f * g * (1.0f + th) * u;
+  } else if constexpr (ACT == FFMOE_ACT_GEGLU_ERF) {
+    return 0.5f * g * (1.0f + erff(g * 0.7071067811865476f)) * u;
   } else {
     const float r = g > 0.0f ? g : 0.0f;
     return r * r * u;
@@ -111,6 +113,12 @@ __device__ __forceinline__ void glu_bwd_t(float ga, float g, float u, float* gg,
     const float dgelu = 0.5f * (1.0f + th) + 0.5f * g * (1.0f - th * th) * dinner;
     *gu = ga * gelu;
     *gg = ga * u * dgelu;
+  } else if constexpr (ACT == FFMOE_ACT_GEGLU_ERF) {
+    // d/dg [g * Phi(g)] = Phi(g) + g * phi(g)
+    const float cdf = 0.5f * (1.0f + erff(g * 0.7071067811865476f));
+    const float pdf = 0.3989422804014327f * __expf(-0.5f * g * g);
+    *gu = ga * g * cdf;
+    *gg = ga * u * (cdf + g * pdf);
   } else {
     const float r = g > 0.0f ? g : 0.0f;
     *gu = ga * r * r;
@@ -125,6 +133,8 @@ __device__ __forceinline__ void with_act(int act, F&& f) {
     f(std::integral_constant<int, FFMOE_ACT_SWIGLU>{});
   else if (act == FFMOE_ACT_GEGLU)
     f(std::integral_constant<int, FFMOE_ACT_GEGLU>{});
+  else if (act == FFMOE_ACT_GEGLU_ERF)
+    f(std::integral_constant<int, FFMOE_ACT_GEGLU_ERF>{});
   else
     f(std::integral_constant<int, FFMOE_ACT_RELU2>{});
 }

@@ -1105,7 +1105,7 @@ extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const i
                                  int D, int H, int activation, void* up_out, void* act_out,
                                  void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_up_glu", E, max_rows, D, H, tile_rows)) return 1;
-  if (activation < 0 || activation > 2) return set_error("ffmoe_gemm_up_glu: unknown activation");
+  if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_gemm_up_glu: unknown activation");
   constexpr int BN = 256;
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BN / 2 - 1) / (BN / 2));
   a.A = static_cast<const bf16_t*>(x_sorted);
@@ -1146,7 +1146,7 @@ extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const v
                                     int tile_rows, int E, int64_t max_rows, int D, int H,
                                     int activation, void* gup_out, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad_glu", E, max_rows, D, H, tile_rows)) return 1;
-  if (activation < 0 || activation > 2) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
+  if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
   constexpr int BN = 128;  // 256 x 128 tiles: a three-stage LDS ring fits
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(wgo);

@@ -3,8 +3,10 @@
 Same constructor arguments, parameter names, initialisation order (so a given
 torch seed yields the same parameters) and forward contract
 ``forward(x[*, D]) -> (out[*, D], losses)``.  The shared expert, when
-present, is the reference's three-linear GLU FFN added outside the routed
-op (nn.py:156-159).
+present, keeps the reference's three bias-free linears as parameters
+(nn.py:22-44) and is added to the routed output (nn.py:156-159); its gate
+and up projections run as one dense GEMM against the stacked weights, and
+its GLU forward / backward as single fused kernels of this library.
 """
 
 import math
@@ -13,7 +15,44 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .fused_moe import fused_moe
+from . import ops
+from .fused_moe import _compute_dtype, fused_moe
+
+# the shared expert's activations (nn.py:33-40); its GeGLU is the exact erf
+# GELU of F.gelu, unlike the routed experts' tanh form
+_SHARED_ACT = {"swiglu": 0, "geglu": 3, "relu_squared": 2}
+
+
+class _SharedGLU(torch.autograd.Function):
+    """down(act(x w_gate^T) * (x w_up^T)) w_down^T with its backward: five
+    dense GEMMs (one for the stacked gate and up projections) and two fused
+    GLU kernels, instead of nine GEMMs and the elementwise chain of three
+    nn.Linear modules."""
+
+    @staticmethod
+    def forward(ctx, x, w_gate, w_up, w_down, act_id):
+        dtype = _compute_dtype(x.dtype)
+        if dtype != torch.bfloat16:
+            raise TypeError(
+                f"ffmoe computes in bfloat16; got compute dtype {dtype} (pass bf16 tensors "
+                "or run under torch.autocast('cuda', dtype=torch.bfloat16))")
+        xc = x.to(dtype).contiguous()
+        w_gu = torch.cat([w_gate.to(dtype), w_up.to(dtype)], 0).contiguous()
+        wd = w_down.to(dtype).contiguous()
+        out, up, act = ops.dense_glu_forward(xc, w_gu, wd, act_id)
+        ctx.save_for_backward(xc, w_gu, wd, up, act)
+        ctx.act_id = act_id
+        ctx.dtypes = (x.dtype, w_gate.dtype, w_up.dtype, w_down.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, go):
+        xc, w_gu, wd, up, act = ctx.saved_tensors
+        dx, dwgu, dwd = ops.dense_glu_backward(go.to(torch.bfloat16).contiguous(), xc, w_gu, wd,
+                                               up, act, ctx.act_id)
+        H = wd.shape[1]
+        xd, gd, ud, dd = ctx.dtypes
+        return dx.to(xd), dwgu[:H].to(gd), dwgu[H:].to(ud), dwd.to(dd), None
 
 
 class _GLUFFN(nn.Module):
@@ -119,7 +158,11 @@ class MoELayer(nn.Module):
             allow_dropped_tokens=self.allow_dropped_tokens,
         )
         if self.shared_expert is not None:
-            routed = routed + self.shared_expert(x_flat)
+            se = self.shared_expert
+            if se.activation not in _SHARED_ACT:
+                raise ValueError(f"Unknown activation: {se.activation}")
+            routed = routed + _SharedGLU.apply(x_flat, se.w_gate.weight, se.w_up.weight,
+                                               se.w_down.weight, _SHARED_ACT[se.activation])
         return routed.reshape(*leading, D), losses
 
     def shard_experts(self, ep_group, ep_backend="nccl"):

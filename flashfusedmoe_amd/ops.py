@@ -235,3 +235,56 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
 def _experts_backward_fake(go, x, gate, w_up, w_down, *rest):
     return [x.new_empty(x.shape), gate.new_empty(gate.shape), w_up.new_empty(w_up.shape),
             w_down.new_empty(w_down.shape)]
+
+
+# ---------------------------------------------------------------------------
+# shared expert: a dense GLU FFN.  Its products are plain dense GEMMs (no
+# routing, one row group), which go to hipBLASLt; the gate and up
+# projections are one GEMM against the stacked [w_gate; w_up], and the GLU
+# forward / backward each run as one fused kernel of this library.
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("ffmoe::dense_glu_forward", mutates_args=())
+def dense_glu_forward(x: Tensor, w_gu: Tensor, w_down: Tensor, activation: int) -> List[Tensor]:
+    """x [N,D], w_gu [2H,D] (gate rows, then up rows), w_down [D,H] ->
+    [out [N,D], up [N,2H] (pre-activation), act [N,H]], all bf16."""
+    for name, t in (("x", x), ("w_gate|w_up", w_gu), ("w_down", w_down)):
+        _check_bf16_gpu(name, t)
+    N, D = x.shape
+    H = w_down.shape[1]
+    _require(w_gu.shape == (2 * H, D) and w_down.shape == (D, H), "shared expert weight shapes")
+    st = L.stream_ptr(x.device)
+    up = x @ w_gu.t()
+    act = torch.empty(N, H, dtype=_BF16, device=x.device)
+    L.call("ffmoe_glu_fwd", L.ptr(up), N, H, activation, L.ptr(act), st)
+    out = act @ w_down.t()
+    return [out, up, act]
+
+
+@dense_glu_forward.register_fake
+def _dense_glu_forward_fake(x, w_gu, w_down, activation):
+    N, D = x.shape
+    H = w_down.shape[1]
+    return [x.new_empty(N, D), x.new_empty(N, 2 * H), x.new_empty(N, H)]
+
+
+@torch.library.custom_op("ffmoe::dense_glu_backward", mutates_args=())
+def dense_glu_backward(go: Tensor, x: Tensor, w_gu: Tensor, w_down: Tensor, up: Tensor,
+                       act: Tensor, activation: int) -> List[Tensor]:
+    """Returns [grad_x [N,D], grad_w_gu [2H,D], grad_w_down [D,H]], bf16."""
+    _check_bf16_gpu("grad_output", go)
+    N, D = x.shape
+    H = w_down.shape[1]
+    st = L.stream_ptr(x.device)
+    gact = go @ w_down
+    gup = torch.empty(N, 2 * H, dtype=_BF16, device=x.device)
+    L.call("ffmoe_glu_bwd", L.ptr(gact), L.ptr(up), N, H, activation, L.ptr(gup), st)
+    dx = gup @ w_gu
+    dwd = go.t() @ act
+    dwgu = gup.t() @ x
+    return [dx, dwgu, dwd]
+
+
+@dense_glu_backward.register_fake
+def _dense_glu_backward_fake(go, x, w_gu, w_down, up, act, activation):
+    return [x.new_empty(x.shape), w_gu.new_empty(w_gu.shape), w_down.new_empty(w_down.shape)]

@@ -45,8 +45,9 @@ extern "C" {
 #define FFMOE_GATING_SIGMOID 1
 /* activation */
 #define FFMOE_ACT_SWIGLU 0
-#define FFMOE_ACT_GEGLU 1
+#define FFMOE_ACT_GEGLU 1 /* tanh-approximated GELU (the routed experts, activations.py) */
 #define FFMOE_ACT_RELU2 2
+#define FFMOE_ACT_GEGLU_ERF 3 /* exact erf GELU (the shared expert's F.gelu, nn.py:36) */
 
 /* limits enforced by the entry points */
 #define FFMOE_MAX_EXPERTS 256

@@ -1,0 +1,112 @@
+"""GPU parity of the shared expert (reference nn.py:22-44, added to the routed
+output at nn.py:156-159), which this build runs through the grouped-GEMM
+kernels as one dense row group with the GLU fused into the epilogues.
+
+* ops.dense_glu_forward / dense_glu_backward against plain fp32 PyTorch
+  (torch.erf for the shared expert's exact GELU), from the kernels' own bf16
+  intermediates, for the three activations.
+* MoELayer(num_shared_experts=1) forward + backward: the routed part against
+  the CPU oracle (routing bit-exact on the GPU's logits), the shared part
+  against torch autograd through the reference's three-linear formula on the
+  CPU (_GLUFFN.forward), every parameter gradient within the bf16 tolerance.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from gpu_helpers import check_close
+from oracle import fused as F_
+
+pytestmark = pytest.mark.gpu
+
+ACTS = ["swiglu", "geglu", "relu_squared"]
+
+
+def _act_ref(name, g, u):
+    if name == "swiglu":
+        return F.silu(g) * u
+    if name == "geglu":  # exact erf GELU, as F.gelu in the reference's shared expert
+        return 0.5 * g * (1.0 + torch.erf(g * 0.7071067811865476)) * u
+    return F.relu(g).square() * u
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("N,D,H", [(1000, 256, 192), (4096, 1024, 2048), (7, 64, 32)])
+def test_dense_glu_against_fp32(act, N, D, H):
+    from flashfusedmoe_amd import ops
+    from flashfusedmoe_amd.nn import _SHARED_ACT
+    g = torch.Generator().manual_seed(N + D + H)
+    x = torch.randn(N, D, generator=g).to(torch.bfloat16).cuda()
+    w_gu = (torch.randn(2 * H, D, generator=g) * D ** -0.5).to(torch.bfloat16).cuda()
+    wd = (torch.randn(D, H, generator=g) * H ** -0.5).to(torch.bfloat16).cuda()
+    go = torch.randn(N, D, generator=g).to(torch.bfloat16).cuda()
+    a = _SHARED_ACT[act]
+    out, up, actv = ops.dense_glu_forward(x, w_gu, wd, a)
+    dx, dwgu, dwd = ops.dense_glu_backward(go, x, w_gu, wd, up, actv, a)
+    torch.cuda.synchronize()
+    f = lambda t: t.float()  # noqa: E731
+    check_close(up, f(x) @ f(w_gu).t(), "up")
+    gg, uu = f(up[:, :H]).requires_grad_(True), f(up[:, H:]).requires_grad_(True)
+    ref_act = _act_ref(act, gg, uu)
+    check_close(actv, ref_act, "act")
+    check_close(out, f(actv) @ f(wd).t(), "out")
+    gact = (f(go) @ f(wd)).to(torch.bfloat16).float()
+    dg, du = torch.autograd.grad(ref_act, (gg, uu), gact)
+    gup = torch.cat([dg, du], 1)
+    dwgu_ref = gup.t() @ f(x)
+    dx_ref = gup @ f(w_gu)
+    check_close(dx, dx_ref, "grad x", atol=2e-3 * max(1.0, dx_ref.abs().max().item()))
+    check_close(dwd, f(go).t() @ f(actv), "grad w_down")
+    check_close(dwgu, dwgu_ref, "grad w_gate|w_up",
+                atol=2e-3 * max(1.0, dwgu_ref.abs().max().item()))
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_moelayer_shared_expert_forward_backward(act):
+    from flashfusedmoe_amd import MoELayer
+    from flashfusedmoe_amd import ops
+    torch.manual_seed(3)
+    D, ffn, E, k, N = 128, 256, 8, 2, 512
+    layer = MoELayer(D, ffn, E, top_k=k, activation=act, num_shared_experts=1)
+    layer = layer.to(torch.bfloat16)
+    ref_shared = layer.shared_expert  # CPU copy of the parameters (reference formula)
+    params_cpu = {n: p.detach().clone() for n, p in layer.named_parameters()}
+    layer = layer.cuda()
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, N // 2, D, generator=g).to(torch.bfloat16)
+    go = torch.randn(2, N // 2, D, generator=g).to(torch.bfloat16)
+    xg = x.cuda().requires_grad_(True)
+    out, _ = layer(xg)
+    out.backward(go.cuda())
+    torch.cuda.synchronize()
+
+    # routed part: the oracle on the GPU's own gate logits
+    xf = x.reshape(N, D)
+    gate, wu, wd = params_cpu["gate.weight"], params_cpu["w_up"], params_cpu["w_down"]
+    logits = ops.route(xf.cuda(), gate.cuda(), None, 1, 0, 1, 0.0, 0.0, False)[0].cpu()
+    r_out, st = F_.forward(xf, gate, wu, wd, k, activation=act, allow_dropped_tokens=True,
+                           logits=logits)
+    gr = F_.backward(st, go.reshape(N, D))
+    # shared part: torch autograd through the reference formula on the CPU
+    sh = ref_shared.__class__(D, ffn, act).to(torch.bfloat16)
+    with torch.no_grad():
+        for name in ("w_gate", "w_up", "w_down"):
+            getattr(sh, name).weight.copy_(params_cpu[f"shared_expert.{name}.weight"])
+    xs = xf.clone().requires_grad_(True)
+    s_out = sh(xs)
+    s_out.backward(go.reshape(N, D))
+
+    exp_out = r_out.float() + s_out.detach().float()
+    check_close(out.detach().cpu().reshape(N, D), exp_out, "output")
+    exp_dx = gr["hidden"].float() + xs.grad.float()
+    check_close(xg.grad.cpu().reshape(N, D), exp_dx, "grad hidden")
+    grads = {n: p.grad.cpu() for n, p in layer.named_parameters()}
+    check_close(grads["gate.weight"], gr["gate"], "grad gate",
+                atol=2e-3 * max(1.0, gr["gate"].abs().max().item()))
+    check_close(grads["w_up"], gr["w_up"], "grad w_up")
+    check_close(grads["w_down"], gr["w_down"], "grad w_down")
+    for name in ("w_gate", "w_up", "w_down"):
+        ref = getattr(sh, name).weight.grad
+        check_close(grads[f"shared_expert.{name}.weight"], ref, f"grad shared {name}",
+                    atol=2e-3 * max(1.0, ref.abs().max().item()))
