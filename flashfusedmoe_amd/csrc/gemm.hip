@@ -529,11 +529,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 
 // Which part of a tile's K range a block computes.  ROLE_FULL: all of it,
-// then the epilogue.  ROLE_PART: the later part; the fp32 partial goes to the
-// block's workspace slot and its flag is raised.  ROLE_OWNER: the first part;
-// the owner adds the partner block's partial (owner + partner, the same sum
-// whichever finishes first) and runs the epilogue.
-enum Role { ROLE_FULL = 0, ROLE_OWNER = 1, ROLE_PART = 2 };
+// then the epilogue.  ROLE_CUT: one of the two K ranges of a tile cut
+// between two blocks.  Both count themselves in on the tile's counter; the
+// first to arrive publishes its fp32 partial (and which slot holds it) and
+// is done, the second waits for that publication (its writer is already
+// running, so no co-residency is needed), adds the partial (two terms: the
+// same bits in either order) and runs the epilogue.
+enum Role { ROLE_FULL = 0, ROLE_CUT = 1 };
 
 struct TileCoord {
   int e, m0, n0, row_begin, row_end;
@@ -593,7 +595,7 @@ constexpr int kDeviceScope = 16;
 // pass); the kernels below loop over tiles with it.
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
 __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord& tc, int k0, int k1,
-                                             int role, int slot, int partner) {
+                                             int role, int slot, int key) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int A_EL = BM * DL_BK, B_EL = BN * DL_BK;  // elements per stage tile
@@ -822,56 +824,69 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   wait_vmcnt_le(0);
   __syncthreads();
 
-  if (role == ROLE_PART) {
-    // publish the fp32 partial: coalesced 16-byte stores in register order.
-    // They are device-scope stores (sc1: written through to the level all
-    // XCDs share, as relaxed agent-scope atomic stores are), so completing
-    // them (vmcnt 0) is all that must precede the flag; no L2 write-back is
-    // needed.  Buffer stores take each store's offset from a scalar constant,
-    // so no address registers are kept per store.
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part + static_cast<int64_t>(slot) * NF * kThreads * 4,
-                                                NF * kThreads * 16);
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4_t v = {acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
-                             acc[tm][tn][4 * q + 3]};
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rp, tid * 16,
-                                                 ((tm * TN + tn) * 4 + q) * kThreads * 16, kDeviceScope);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // one 32x32 tile of accumulator reads at a time
-      }
-    wait_vmcnt_le(0);
+  // cut tile: counter flags[key], publication flags[G + key] (= slot + 1)
+  int partner = 0;
+  if (role == ROLE_CUT) {
+    int* s_word = reinterpret_cast<int*>(smem);
+    if (tid == 0)
+      *s_word = __hip_atomic_fetch_add(p.flags + key, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (tid == 0) __hip_atomic_store(p.flags + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-  if (role == ROLE_OWNER) {
-    // wait for the later part (a tile is cut at most once: every stream-K
-    // range is at least one tile long), which the staging below adds; the
-    // flag is cleared once consumed, so the flags are all zero again when the
-    // launch ends
+    const bool first = *s_word == 0;
+    __syncthreads();
+    if (first) {
+      // publish the fp32 partial: coalesced 16-byte stores in register
+      // order.  They are device-scope stores (sc1: written through to the
+      // level all XCDs share, as relaxed agent-scope atomic stores are), so
+      // completing them (vmcnt 0) is all that must precede the publication;
+      // no L2 write-back is needed.  Buffer stores take each store's offset
+      // from a scalar constant, so no address registers are kept per store.
+      const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part + static_cast<int64_t>(slot) * NF * kThreads * 4,
+                                                  NF * kThreads * 16);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4_t v = {acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
+                               acc[tm][tn][4 * q + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rp, tid * 16,
+                                                   ((tm * TN + tn) * 4 + q) * kThreads * 16, kDeviceScope);
+          }
+          __builtin_amdgcn_sched_barrier(0);  // one 32x32 tile of accumulator reads at a time
+        }
+      wait_vmcnt_le(0);
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_store(p.flags + gridDim.x + key, slot + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    // second arrival: wait for the publication (bounded: its writer is past
+    // the counter, i.e. running), then clear both words for the next launch
     if (tid == 0) {
-      int polls = 0;
-      while (__hip_atomic_load(p.flags + partner, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
+      int src = 0, polls = 0;
+      while ((src = __hip_atomic_load(p.flags + gridDim.x + key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0 &&
              ++polls < kSpinLimit)
         __builtin_amdgcn_s_sleep(8);
-      __hip_atomic_store(p.flags + partner, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (polls >= kSpinLimit)  // never expected: report through the error word
-        __hip_atomic_store(p.flags + gridDim.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.flags + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.flags + gridDim.x + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (polls >= kSpinLimit) {  // never expected: report through the error word
+        __hip_atomic_store(p.flags + 2 * gridDim.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        src = slot + 1;  // add nothing meaningful rather than read a wild slot
+      }
+      *s_word = src - 1;
     }
     __syncthreads();  // the partial is read below with device-scope loads
+    partner = *s_word;
+    __syncthreads();
   }
 
   // epilogue: every wave stages its bf16 accumulators in the LDS C tile (one
   // 32x32 MFMA tile at a time; the scheduling barriers keep the compiler from
   // hoisting all accumulator reads, which would spill), then the block stores
   // the whole tile
-  // (an owner adds its partner's fp32 partial here, so the accumulators are
-  // only ever written by the MFMAs)
+  // (the second block of a cut tile adds the first's fp32 partial here, so
+  // the accumulators are only ever written by the MFMAs)
   bf16_t* Cs = smem;
   const int lr = lane & 31;
   const int lq = (lane >> 5) * 4;
@@ -911,7 +926,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   constexpr int PIT = (EPI == EPI_GLU_BWD) ? glu_bwd_items<BM, BN>() : 1;
   uint4 pre_g[PIT], pre_u[PIT];
   if constexpr (EPI == EPI_GLU_BWD) glu_bwd_prefetch<BM, BN>(p, row_begin, row_end, n0, pre_g, pre_u);
-  if (role == ROLE_OWNER) stage(std::true_type{});
+  if (role == ROLE_CUT) stage(std::true_type{});
   else stage(std::false_type{});
   __syncthreads();
   if constexpr (EPI == EPI_GLU_BWD)
@@ -933,13 +948,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
   gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
 }
 
-// Persistent grouped-rows GEMM, one block per CU (cooperative launch, so all
-// blocks are resident and a flag wait always ends).  The R x n_tiles tiles
+// Persistent grouped-rows GEMM, one block per CU.  The R x n_tiles tiles
 // (R = tile_offsets[E], read on the device) are split into whole-tile rounds
 // of G tiles, one per block, and a stream-K tail: the last T - (T/G - 1)*G
 // tiles' K steps are cut into G equal contiguous ranges, so every block gets
 // the same work and block epilogues fall at different times.  A tile cut
-// between blocks is finished by the block holding its first K step.
+// between two blocks is finished by whichever of them gets there second
+// (ROLE_CUT); a block only ever waits for one that is already running, so
+// the launch needs no co-residency guarantee.
 template <int BM, int BN, bool A_KC, bool B_KC, int EPI>
 __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
@@ -960,7 +976,7 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
   // one call site for every work item keeps a single copy of the tile code
   for (;;) {
     int64_t t;
-    int k0 = 0, k1 = nk, role = ROLE_FULL;
+    int k0 = 0, k1 = nk, role = ROLE_FULL, key = v;
     if (r < rounds) {
       t = r * G + v;
       ++r;
@@ -971,9 +987,10 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
       const int64_t rest = gend - g;
       k1 = rest < nk - k0 ? k0 + static_cast<int>(rest) : nk;
       if (k0 > 0) {
-        role = ROLE_PART;  // a block's first range only
+        role = ROLE_CUT;  // a block's first range only; block v - 1 holds [0, k0)
+        key = v - 1;
       } else if (k1 < nk) {
-        role = ROLE_OWNER;  // block v + 1 holds K steps [k1, nk) of this tile
+        role = ROLE_CUT;  // block v + 1 holds K steps [k1, nk) of this tile
       }
       t = base + ts;
       g += k1 - k0;
@@ -981,7 +998,7 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
       break;
     }
     const TileCoord tc = decode_rows_tile<BM, BN>(p, t, R);
-    gemm_dl_tile<BM, BN, A_KC, B_KC, 0, EPI>(p, tc, k0, k1, role, v, v + 1);
+    gemm_dl_tile<BM, BN, A_KC, B_KC, 0, EPI>(p, tc, k0, k1, role, v, key);
   }
 #endif
 }
@@ -1015,7 +1032,7 @@ static int launch(const GemmArgs& a, hipStream_t st, const char* name) {
 // Persistent blocks per device: one per CU.
 constexpr int kMaxSkBlocks = 1023;
 constexpr int kSkMinK = 4096;
-constexpr int64_t kSkFlagBytes = 4096;  // int32 flags [G] + error word, zero on entry
+constexpr int64_t kSkFlagBytes = 8192;  // int32 counters [G], publications [G], error word; zero on entry
 constexpr int64_t kSkSlotBytes = 256 * 256 * 4;  // fp32 partial of the largest tile
 
 static int sk_blocks() {
@@ -1042,12 +1059,8 @@ static int launch_sk(GemmArgs a, void* ws, hipStream_t st, const char* name) {
   if (G <= 0) return set_error(std::string(name) + ": cannot query the CU count");
   a.flags = static_cast<int*>(ws);
   a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kSkFlagBytes);
-  void* args[] = {&a};
-  const hipError_t err = hipLaunchCooperativeKernel(
-      reinterpret_cast<const void*>(&gemm_sk_kernel<BM, BN, true, B_KC, EPI>), dim3(G),
-      dim3(kThreads), args, 0, st);
-  if (err != hipSuccess)
-    return set_error(std::string(name) + ": cooperative launch failed: " + hipGetErrorString(err));
+  hipLaunchKernelGGL((gemm_sk_kernel<BM, BN, true, B_KC, EPI>), dim3(G), dim3(kThreads), 0, st, a);
+  if (check_launch(name)) return 1;
   return clear_error();
 }
 

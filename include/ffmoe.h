@@ -171,7 +171,7 @@ int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
 int ffmoe_gemm_tile_rows(int64_t max_rows, int E);
 
 /* Bytes of the `sk_workspace` the four grouped-rows GEMMs below take on the
- * current device (-1 if the device cannot be queried).  Its first 4 KiB are
+ * current device (-1 if the device cannot be queried).  Its first 8 KiB are
  * int32 flags that must be zero before the first call; every call leaves them
  * zero again, so one workspace serves any number of calls in stream order.
  * Calls that may overlap (different streams) need separate workspaces.
