@@ -998,7 +998,9 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
       break;
     }
     const TileCoord tc = decode_rows_tile<BM, BN>(p, t, R);
-    gemm_dl_tile<BM, BN, A_KC, B_KC, 0, EPI>(p, tc, k0, k1, role, v, key);
+    // a block may publish for both of its cut tiles (the end of one, then the
+    // start of another) before either partner reads: one slot for each
+    gemm_dl_tile<BM, BN, A_KC, B_KC, 0, EPI>(p, tc, k0, k1, role, 2 * v + (k0 == 0 ? 1 : 0), key);
   }
 #endif
 }
@@ -1104,7 +1106,7 @@ extern "C" int ffmoe_gemm_tile_rows(int64_t max_rows, int E) {
 
 extern "C" int64_t ffmoe_gemm_workspace_bytes(void) {
   const int G = sk_blocks();
-  return G > 0 ? kSkFlagBytes + static_cast<int64_t>(G) * kSkSlotBytes : -1;
+  return G > 0 ? kSkFlagBytes + 2 * static_cast<int64_t>(G) * kSkSlotBytes : -1;
 }
 
 extern "C" int ffmoe_set_lds_transpose(int enable) {

@@ -84,3 +84,79 @@ def expected_rows(idx, E, mt, capacity_mode):
     if not capacity_mode and counts[0] > 0:
         out = np.where(own, out, -2)
     return out, counts, off
+
+
+def moe_reference(x, gate, wu, wd, idx, w, go=None, activation="swiglu", wgrad_experts=None):
+    """fp32 PyTorch restatement on the GPU of the fused MoE forward and
+    backward for a given routing (idx [N,k] int64, w [N,k] fp32), with the
+    oracle's rounding points (oracle/fused.py forward/backward): up, act and
+    down rounded to bf16; the combine in fp32 slot order with bf16 weights;
+    the weighted grad rows go*bf16(w) rounded to bf16; the top-k softmax
+    backward in fp32 over the selected slots; grad_logits rounded to bf16
+    before both gate products.  No token is dropped; no aux / z terms.
+    Returns dict(out, dx, dgate, dwu, dwd), the weight gradients as
+    {expert: tensor} for wgrad_experts (default: all)."""
+    from oracle import fused as F_
+    bf = torch.bfloat16
+    N, D = x.shape
+    E = wu.shape[0]
+    H = wd.shape[2]
+    k = idx.shape[1]
+    T = N * k
+    dev = x.device
+    flat = idx.reshape(-1)
+    order = torch.argsort(flat, stable=True)
+    counts = torch.bincount(flat, minlength=E).tolist()
+    starts = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    pos = torch.empty_like(order)
+    pos[order] = torch.arange(T, device=dev)
+    xs = x[order // k]
+    up = torch.empty(T, 2 * H, dtype=bf, device=dev)
+    act = torch.empty(T, H, dtype=bf, device=dev)
+    down = torch.empty(T, D, dtype=bf, device=dev)
+    for e in range(E):
+        r0, r1 = int(starts[e]), int(starts[e + 1])
+        if r1 > r0:
+            up[r0:r1] = F_.gemm(xs[r0:r1], wu[e].t())
+            act[r0:r1] = F_.glu_forward(up[r0:r1], activation)
+            down[r0:r1] = F_.gemm(act[r0:r1], wd[e].t())
+    wb = w.to(bf).float()
+    dn = down[pos].view(N, k, D).float()
+    acc = torch.zeros(N, D, device=dev)
+    for s in range(k):
+        acc = acc + dn[:, s] * wb[:, s:s + 1]
+    res = {"out": acc.to(bf)}
+    if go is None:
+        return res
+    gof = go.float()
+    g_w = (dn * gof[:, None, :]).sum(-1)
+    del dn, acc
+    wgo = (gof[:, None, :] * wb[:, :, None]).to(bf).view(T, D)[order]
+    gup = torch.empty(T, 2 * H, dtype=bf, device=dev)
+    ghb = torch.empty(T, D, dtype=bf, device=dev)
+    experts = set(range(E) if wgrad_experts is None else wgrad_experts)
+    dwu, dwd = {}, {}
+    for e in range(E):
+        r0, r1 = int(starts[e]), int(starts[e + 1])
+        if r1 > r0:
+            gact = F_.gemm(wgo[r0:r1], wd[e])
+            gup[r0:r1] = F_.glu_backward(gact, up[r0:r1], activation)
+            ghb[r0:r1] = F_.gemm(gup[r0:r1], wu[e])
+        if e in experts:
+            if r1 > r0:
+                dwd[e] = F_.gemm(wgo[r0:r1].t(), act[r0:r1])
+                dwu[e] = F_.gemm(gup[r0:r1].t(), xs[r0:r1])
+            else:
+                dwd[e] = torch.zeros(D, H, dtype=bf, device=dev)
+                dwu[e] = torch.zeros(2 * H, D, dtype=bf, device=dev)
+    rows = ghb[pos].view(N, k, D).float()
+    gh = torch.zeros(N, D, device=dev)
+    for s in range(k):
+        gh = gh + rows[:, s]
+    gh = gh.to(bf)
+    gtl = w * (g_w - (g_w * w).sum(-1, keepdim=True))
+    gl = torch.zeros(N, E, device=dev).scatter_add_(1, idx, gtl).to(bf)
+    res["dx"] = (gh.float() + F_.gemm(gl, gate).float()).to(bf)
+    res["dgate"] = F_.gemm(gl.t().contiguous(), x)
+    res["dwu"], res["dwd"] = dwu, dwd
+    return res
