@@ -1049,13 +1049,14 @@ static int sk_blocks() {
   return cached[dev];
 }
 
+// min_k: the persistent schedule is used from this K on.  It moves an fp32
+// partial (BM x BN x 4 bytes, written and read once) for every cut tile, so
+// it pays where the partial is small against the tile's operand bytes; below
+// min_k the GEMM runs one block per tile.
 template <int BM, int BN, bool B_KC, int EPI>
-static int launch_sk(GemmArgs a, void* ws, hipStream_t st, const char* name) {
+static int launch_sk(GemmArgs a, void* ws, int min_k, hipStream_t st, const char* name) {
   if (a.total_tiles <= 0) return clear_error();
-  // The persistent schedule costs some per-tile efficiency (measured ~10%)
-  // and moves fp32 partials for cut tiles; it pays where a tile is long
-  // (K >= kSkMinK), so a mostly empty last round of whole tiles costs more.
-  if (ws == nullptr || a.K % DL_BK != 0 || a.K < kSkMinK || !g_use_tr)
+  if (ws == nullptr || a.K % DL_BK != 0 || a.K < min_k || !g_use_tr)
     return launch<BM, BN, true, B_KC, 0, EPI>(a, st, name);
   const int G = sk_blocks();
   if (G <= 0) return set_error(std::string(name) + ": cannot query the CU count");
@@ -1069,9 +1070,10 @@ static int launch_sk(GemmArgs a, void* ws, hipStream_t st, const char* name) {
 // Grouped-rows launch with the row-tile height the caller's tile_offsets were
 // computed for.
 template <int BN, bool B_KC, int EPI>
-static int launch_rows(const GemmArgs& a, int tile_rows, void* ws, hipStream_t st, const char* name) {
-  if (tile_rows == 256) return launch_sk<256, BN, B_KC, EPI>(a, ws, st, name);
-  return launch_sk<128, BN, B_KC, EPI>(a, ws, st, name);
+static int launch_rows(const GemmArgs& a, int tile_rows, void* ws, int min_k, hipStream_t st,
+                       const char* name) {
+  if (tile_rows == 256) return launch_sk<256, BN, B_KC, EPI>(a, ws, min_k, st, name);
+  return launch_sk<128, BN, B_KC, EPI>(a, ws, min_k, st, name);
 }
 
 static GemmArgs rows_args(const int32_t* offsets, const int32_t* tile_offsets, int E,
@@ -1135,7 +1137,10 @@ extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const i
   a.K = D;
   a.H = H;
   a.act = activation;
-  return launch_rows<BN, true, EPI_GLU_FWD>(a, tile_rows, sk_workspace, static_cast<hipStream_t>(stream), "gemm_up_glu");
+  // 256 x 256 tiles, K = D: stream-K only for long K (its cut-tile partials
+  // cost more than the whole-tile tail round at D = 1024, measured)
+  return launch_rows<BN, true, EPI_GLU_FWD>(a, tile_rows, sk_workspace, kSkMinK,
+                                            static_cast<hipStream_t>(stream), "gemm_up_glu");
 }
 
 extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
@@ -1153,7 +1158,8 @@ extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_
   a.b_stride = static_cast<int64_t>(D) * H;
   a.N = D;
   a.K = H;
-  return launch_rows<BN, true, EPI_STORE>(a, tile_rows, sk_workspace, static_cast<hipStream_t>(stream), "gemm_down");
+  return launch_rows<BN, true, EPI_STORE>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
+                                          "gemm_down");
 }
 
 extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,
@@ -1176,7 +1182,7 @@ extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const v
   a.K = D;
   a.H = H;
   a.act = activation;
-  return launch_rows<BN, false, EPI_GLU_BWD>(a, tile_rows, sk_workspace, static_cast<hipStream_t>(stream),
+  return launch_rows<BN, false, EPI_GLU_BWD>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
                                              "gemm_dgrad_glu");
 }
 
@@ -1184,7 +1190,7 @@ extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t
                                 const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
                                 int H, int D, void* ghb_out, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad", E, max_rows, D, H, tile_rows)) return 1;
-  constexpr int BN = 128;  // 256 x 128 tiles: a three-stage LDS ring fits
+  constexpr int BN = 256;  // 256 x 256 tiles (two stages) under the stream-K schedule
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(gup);
   a.B = static_cast<const bf16_t*>(w_up);
@@ -1195,7 +1201,8 @@ extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t
   a.b_stride = static_cast<int64_t>(2) * H * D;
   a.N = D;
   a.K = 2 * H;
-  return launch_rows<BN, false, EPI_STORE>(a, tile_rows, sk_workspace, static_cast<hipStream_t>(stream), "gemm_dgrad");
+  return launch_rows<BN, false, EPI_STORE>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
+                                           "gemm_dgrad");
 }
 
 extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
