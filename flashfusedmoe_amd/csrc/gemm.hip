@@ -971,8 +971,12 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
   const int64_t iters = (T - base) * nk;
   const int64_t S = (iters + G - 1) / G;
   int64_t r = 0;                 // next whole-tile round
-  int64_t g = v * S;             // next K step of the stream-K range
-  const int64_t gend = g + S < iters ? g + S : iters;
+  // The stream-K range [g, gend) is walked from its end: every block then
+  // starts its range at K step 0 of a tile at the same moment, so the blocks
+  // sharing A rows or B columns read the same K slices together (L2 hits);
+  // walked forwards, each block would start at its own K offset.
+  const int64_t g = v * S;
+  int64_t gcur = g + S < iters ? g + S : iters;
   // one call site for every work item keeps a single copy of the tile code
   for (;;) {
     int64_t t;
@@ -981,25 +985,25 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
       t = r * G + v;
       ++r;
       if (t >= base) continue;
-    } else if (g < gend) {
-      const int64_t ts = g / nk;
-      k0 = static_cast<int>(g - ts * nk);
-      const int64_t rest = gend - g;
-      k1 = rest < nk - k0 ? k0 + static_cast<int>(rest) : nk;
+    } else if (gcur > g) {
+      const int64_t ts = (gcur - 1) / nk;
+      const int64_t tstart = ts * nk;
+      k0 = static_cast<int>((g > tstart ? g : tstart) - tstart);
+      k1 = static_cast<int>(gcur - tstart);
       if (k0 > 0) {
-        role = ROLE_CUT;  // a block's first range only; block v - 1 holds [0, k0)
+        role = ROLE_CUT;  // the range's first tile; block v - 1 holds [0, k0)
         key = v - 1;
       } else if (k1 < nk) {
-        role = ROLE_CUT;  // block v + 1 holds K steps [k1, nk) of this tile
+        role = ROLE_CUT;  // the range's last tile; block v + 1 holds [k1, nk)
       }
       t = base + ts;
-      g += k1 - k0;
+      gcur = tstart + k0;
     } else {
       break;
     }
     const TileCoord tc = decode_rows_tile<BM, BN>(p, t, R);
-    // a block may publish for both of its cut tiles (the end of one, then the
-    // start of another) before either partner reads: one slot for each
+    // a block may publish for both of its cut tiles (the start of one, then
+    // the end of another) before either partner reads: one slot for each
     gemm_dl_tile<BM, BN, A_KC, B_KC, 0, EPI>(p, tc, k0, k1, role, 2 * v + (k0 == 0 ? 1 : 0), key);
   }
 #endif
