@@ -205,6 +205,11 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     ws = L.ptr(L.gemm_workspace(dev, st))
     L.call("ffmoe_gemm_dgrad_glu", L.ptr(wgo), L.ptr(w_down), L.ptr(up), L.ptr(offsets),
            L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(gup), ws, st)
+    # the up-projection weight gradient right after the GEMM that wrote `gup`
+    # (128 MiB at C2) while it is still cache-resident; measured ~1% faster
+    # per step than after the dX GEMMs
+    dwu = torch.empty(E, H2, D, dtype=_BF16, device=dev)
+    L.call("ffmoe_gemm_wgrad", L.ptr(gup), L.ptr(xs), L.ptr(offsets), E, H2, D, L.ptr(dwu), st)
     ghb = torch.empty(T, D, dtype=_BF16, device=dev)
     L.call("ffmoe_gemm_dgrad", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
            T, H, D, L.ptr(ghb), ws, st)
@@ -219,8 +224,6 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
                st)
     dwd = torch.empty(E, D, H, dtype=_BF16, device=dev)
     L.call("ffmoe_gemm_wgrad", L.ptr(wgo), L.ptr(act), L.ptr(offsets), E, D, H, L.ptr(dwd), st)
-    dwu = torch.empty(E, H2, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_wgrad", L.ptr(gup), L.ptr(xs), L.ptr(offsets), E, H2, D, L.ptr(dwu), st)
     if fused_gate:
         dgate = torch.empty(E, D, dtype=_BF16, device=dev)
         part = torch.empty(int(L.load().ffmoe_gate_grad_workspace_bytes(N, D, E)), dtype=torch.uint8,
