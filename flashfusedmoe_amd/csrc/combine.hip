@@ -11,37 +11,74 @@ __device__ __forceinline__ int src_row(int row) {
   return row >= 0 ? row : (row == FFMOE_ROW_ALIAS0 ? 0 : -1);
 }
 
+// Gathers of k rows per token.  A thread owns U 16-byte vectors of one token
+// (v0 + j * nvec/U, j < U): it reads the token's k row indices once, then
+// issues every slot's loads before the first add, so k*U loads are in flight
+// per thread instead of one dependent pair per slot.
+template <int KMAX, int U>
+__device__ __forceinline__ void gather_rows(const bf16_t* __restrict__ rows,
+                                            const int32_t* __restrict__ row_of, int64_t n, int k,
+                                            int nvec, int v0, int nq, int* r, uint4 (*val)[U]) {
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) r[s] = s < k ? src_row(row_of[n * k + s]) : -1;
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      val[s][j] = make_uint4(0, 0, 0, 0);
+      if (r[s] >= 0)
+        val[s][j] = reinterpret_cast<const uint4*>(rows + static_cast<int64_t>(r[s]) * (nvec * 8))[v0 + j * nq];
+    }
+  }
+}
+
 // out[n, 8v:8v+8] = sum_s w_s * rows[src(row_of[n*k+s]), 8v:8v+8], fp32 in
 // slot order (moe_ops.py:156-203), then bf16; optional bf16 addend added after
 // rounding (fused_moe.py:590).
+template <int KMAX, int U>
 __global__ __launch_bounds__(256) void combine_kernel(const bf16_t* __restrict__ rows,
                                                       const int32_t* __restrict__ row_of,
                                                       const float* __restrict__ topk_w,
                                                       const bf16_t* __restrict__ addend, int64_t N,
                                                       int D, int k, bf16_t* __restrict__ out) {
   const int nvec = D / 8;
-  const int64_t total = N * nvec;
+  const int nq = nvec / U;
+  const int64_t total = N * nq;
   for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
        u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t n = u / nvec;
-    const int v = static_cast<int>(u % nvec);
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < k; ++s) {
-      const int r = src_row(row_of[n * k + s]);
-      if (r < 0) continue;
-      const float w = topk_w != nullptr ? round_bf16(topk_w[n * k + s]) : 1.0f;
-      float f[8];
-      unpack8(reinterpret_cast<const uint4*>(rows + static_cast<int64_t>(r) * D)[v], f);
+    const int64_t n = u / nq;
+    const int v0 = static_cast<int>(u % nq);
+    int r[KMAX];
+    uint4 val[KMAX][U];
+    float w[KMAX];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += w * f[i];
-    }
+    for (int s = 0; s < KMAX; ++s)
+      w[s] = (s < k && topk_w != nullptr) ? round_bf16(topk_w[n * k + s]) : 1.0f;
+    gather_rows<KMAX, U>(rows, row_of, n, k, nvec, v0, nq, r, val);
+    uint4 av[U];
     if (addend != nullptr) {
-      float a[8];
-      unpack8(reinterpret_cast<const uint4*>(addend + n * D)[v], a);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = round_bf16(acc[i]) + a[i];
+      for (int j = 0; j < U; ++j) av[j] = reinterpret_cast<const uint4*>(addend + n * D)[v0 + j * nq];
     }
-    reinterpret_cast<uint4*>(out + n * D)[v] = pack8(acc);
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s) {
+        if (r[s] < 0) continue;
+        float f[8];
+        unpack8(val[s][j], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += w[s] * f[i];
+      }
+      if (addend != nullptr) {
+        float a[8];
+        unpack8(av[j], a);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = round_bf16(acc[i]) + a[i];
+      }
+      reinterpret_cast<uint4*>(out + n * D)[v0 + j * nq] = pack8(acc);
+    }
   }
 }
 
@@ -87,119 +124,139 @@ __global__ __launch_bounds__(256) void dx_reduce_kernel(const bf16_t* __restrict
 }
 
 // Gate weight gradient dgate[E, D] = gl^T x (fused_moe.py:591), E <=
-// FFMOE_MAX_FUSED_GATE_E.  Pass 1: a block takes a 256-column slice of
-// kGateChunk tokens; its gl rows are staged in LDS, each of the 4 waves
-// accumulates a quarter of the tokens in token order (lane l owns 4 columns,
-// all of a wave's x loads in flight together), and the 4 wave partials are
-// added in wave order through LDS into one fp32 partial per block.  Pass 2
-// sums the partials in chunk order and rounds to bf16.  x is read once;
-// deterministic.
-constexpr int kGateChunk = 64;
-constexpr int kGateWaves = 4;
-constexpr int kGateBatch = kGateChunk / kGateWaves;
+// FFMOE_MAX_FUSED_GATE_E.  Pass 1: a block takes a kGateCols-column slice of
+// kGateChunk tokens.  Thread (row group rg, vector cv) owns 8 columns and the
+// tokens rg, rg + 16, ...: its x loads and gl-row loads are all issued at
+// once (the block's 32 KiB x tile is in flight together, two blocks per CU).
+// Per batch of 8 experts the 16 row groups are added in row-group order
+// through LDS into one fp32 partial per block.  Pass 2 sums the partials in
+// a fixed order and rounds to bf16.  x is read once; deterministic.
+constexpr int kGateChunk = 128;
+constexpr int kGateCols = 128;
+constexpr int kGateGroups = 256 / (kGateCols / 8);  // row groups per block
+constexpr int kGateTok = kGateChunk / kGateGroups;  // tokens per thread
 
-template <int EMAX>
+__device__ __forceinline__ void gate_gl_row(const bf16_t* __restrict__ gl, int64_t n, int E, int eb,
+                                            bool ok, uint4& packed, float* g) {
+  if ((E & 7) == 0) {
+    packed = ok ? *reinterpret_cast<const uint4*>(gl + n * E + eb) : make_uint4(0, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) g[q] = (ok && eb + q < E) ? bf16_to_f32(gl[n * E + eb + q]) : 0.0f;
+  }
+}
+
 __global__ __launch_bounds__(256) void gate_grad_partial_kernel(const bf16_t* __restrict__ gl,
                                                                 const bf16_t* __restrict__ x,
                                                                 int64_t N, int D, int E,
                                                                 float* __restrict__ part) {
-  __shared__ float s_gl[kGateChunk * EMAX];
-  __shared__ float4 s_red[kGateWaves][8][64];
+  __shared__ float4 s_red[kGateGroups][8][kGateCols / 4];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int c0 = blockIdx.x * 256 + lane * 4;
+  const int rg = tid / (kGateCols / 8), cv = tid % (kGateCols / 8);
+  const int cbase = blockIdx.x * kGateCols;
+  const int col = cbase + cv * 8;
   const int64_t chunk = blockIdx.y;
   const int64_t n0 = chunk * kGateChunk;
   const int nt = static_cast<int>(min<int64_t>(kGateChunk, N - n0));
-  for (int i = tid; i < kGateChunk * E; i += 256)
-    s_gl[i] = i < nt * E ? bf16_to_f32(gl[n0 * E + i]) : 0.0f;
-  __syncthreads();
-  float acc[EMAX][4];
+  const bool col_ok = col < D;  // D % 8 == 0: a vector is wholly in or out
+  uint4 xv[kGateTok];
 #pragma unroll
-  for (int e = 0; e < EMAX; ++e)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[e][i] = 0.0f;
-  const bool col_ok = c0 < D;
-  const int t0 = wave * kGateBatch;
-  uint2 xv[kGateBatch];
-#pragma unroll
-  for (int j = 0; j < kGateBatch; ++j) {
-    const int t = t0 + j;
-    xv[j] = (col_ok && t < nt) ? *reinterpret_cast<const uint2*>(x + (n0 + t) * D + c0)
-                               : make_uint2(0, 0);
+  for (int j = 0; j < kGateTok; ++j) {
+    const int t = rg + j * kGateGroups;
+    xv[j] = (col_ok && t < nt) ? *reinterpret_cast<const uint4*>(x + (n0 + t) * D + col)
+                               : make_uint4(0, 0, 0, 0);
   }
+  for (int eb = 0; eb < E; eb += 8) {
+    uint4 gp[kGateTok];
+    float gf[kGateTok][8];
 #pragma unroll
-  for (int j = 0; j < kGateBatch; ++j) {
-    const int t = t0 + j;
-    float xf[4];
-    xf[0] = __uint_as_float(xv[j].x << 16);
-    xf[1] = __uint_as_float(xv[j].x & 0xffff0000u);
-    xf[2] = __uint_as_float(xv[j].y << 16);
-    xf[3] = __uint_as_float(xv[j].y & 0xffff0000u);
-#pragma unroll
-    for (int e = 0; e < EMAX; ++e) {
-      if (e < E) {
-        const float g = s_gl[t * E + e];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[e][i] += g * xf[i];
-      }
+    for (int j = 0; j < kGateTok; ++j) {
+      const int t = rg + j * kGateGroups;
+      gate_gl_row(gl, n0 + t, E, eb, t < nt, gp[j], gf[j]);
     }
-  }
-  // wave partials -> one block partial, 8 experts at a time, waves in order
+    float acc[8][8];
 #pragma unroll
-  for (int eb = 0; eb < EMAX; eb += 8) {
-    if (eb >= E) break;
+    for (int q = 0; q < 8; ++q)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      s_red[wave][j][lane] = make_float4(acc[eb + j][0], acc[eb + j][1], acc[eb + j][2], acc[eb + j][3]);
+      for (int i = 0; i < 8; ++i) acc[q][i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kGateTok; ++j) {
+      float xf[8];
+      unpack8(xv[j], xf);
+      if ((E & 7) == 0) unpack8(gp[j], gf[j]);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[q][i] += gf[j][q] * xf[i];
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      s_red[rg][q][cv * 2] = make_float4(acc[q][0], acc[q][1], acc[q][2], acc[q][3]);
+      s_red[rg][q][cv * 2 + 1] = make_float4(acc[q][4], acc[q][5], acc[q][6], acc[q][7]);
+    }
     __syncthreads();
-    // thread (wave w, lane l) finishes experts eb + 2w, eb + 2w + 1 of lane l's columns
+    {  // 8 experts x 128 columns, 4 per thread; row groups added in order
+      const int q = tid / (kGateCols / 4), c4 = tid % (kGateCols / 4);
+      float4 r = s_red[0][q][c4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = 2 * wave + h;
-      const int e = eb + j;
-      float4 r = s_red[0][j][lane];
-#pragma unroll
-      for (int w = 1; w < kGateWaves; ++w) {
-        const float4 v = s_red[w][j][lane];
+      for (int w = 1; w < kGateGroups; ++w) {
+        const float4 v = s_red[w][q][c4];
         r.x += v.x;
         r.y += v.y;
         r.z += v.z;
         r.w += v.w;
       }
-      if (col_ok && e < E)
-        *reinterpret_cast<float4*>(part + (chunk * E + e) * static_cast<int64_t>(D) + c0) = r;
+      if (eb + q < E && cbase + c4 * 4 < D)
+        *reinterpret_cast<float4*>(part + (chunk * E + eb + q) * static_cast<int64_t>(D) + cbase + c4 * 4) = r;
     }
     __syncthreads();
   }
 }
 
-// 64 outputs per block, 4 threads per output: thread q sums parts q, q+4, ...
-// in order, then thread 0 of each output adds the four in order.
+// Pass 2: 16 output quads (4 consecutive outputs) per block, 16 threads per
+// quad; thread j sums parts j, j + 16, ... in order (all its loads in
+// flight), then the 16 sums are added in j order.
+constexpr int kGateFinalLoads = 8;
+
 __global__ __launch_bounds__(256) void gate_grad_final_kernel(const float* __restrict__ part,
                                                               int64_t nparts, int D, int E,
                                                               bf16_t* __restrict__ out) {
-  __shared__ float s[256];
+  __shared__ float4 s[16][16];
   const int tid = threadIdx.x;
-  const int q = tid >> 6;
-  const int64_t total = static_cast<int64_t>(E) * D;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 64 + (tid & 63);
-  float acc = 0.0f;
+  const int oq = tid >> 4, j = tid & 15;
+  const int64_t total = static_cast<int64_t>(E) * D;  // a multiple of 8
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 16 + oq) * 4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (i < total) {
-    int64_t c = q;
-    for (; c + 12 < nparts; c += 16) {
-      const float a0 = part[c * total + i], a1 = part[(c + 4) * total + i];
-      const float a2 = part[(c + 8) * total + i], a3 = part[(c + 12) * total + i];
-      acc += a0;
-      acc += a1;
-      acc += a2;
-      acc += a3;
+    for (int64_t c0 = j; c0 < nparts; c0 += 16 * kGateFinalLoads) {
+      float4 v[kGateFinalLoads];
+#pragma unroll
+      for (int u = 0; u < kGateFinalLoads; ++u) {
+        const int64_t c = c0 + 16 * u;
+        v[u] = c < nparts ? *reinterpret_cast<const float4*>(part + c * total + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < kGateFinalLoads; ++u) {
+        if (c0 + 16 * u >= nparts) break;
+        acc.x += v[u].x;
+        acc.y += v[u].y;
+        acc.z += v[u].z;
+        acc.w += v[u].w;
+      }
     }
-    for (; c < nparts; c += 4) acc += part[c * total + i];
   }
-  s[tid] = acc;
+  s[oq][j] = acc;
   __syncthreads();
-  if (q == 0 && i < total) out[i] = f32_to_bf16(((s[tid] + s[tid + 64]) + s[tid + 128]) + s[tid + 192]);
+  if (j == 0 && i < total) {
+    float4 r = s[oq][0];
+    for (int q = 1; q < 16; ++q) {
+      r.x += s[oq][q].x;
+      r.y += s[oq][q].y;
+      r.z += s[oq][q].z;
+      r.w += s[oq][q].w;
+    }
+    *reinterpret_cast<uint2*>(out + i) = make_uint2(pack_bf16x2(r.x, r.y), pack_bf16x2(r.z, r.w));
+  }
 }
 
 // The aux loss's routing when its gradient flows through the routing weights:
@@ -233,36 +290,65 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
   if (n >= N) return;
   const int nvec = D / 8;
   const uint4* gor = reinterpret_cast<const uint4*>(go + n * D);
-  float gw[KMAX];
+  // every slot's row index and weight first; then, per chunk of VC vectors
+  // per lane, the go vectors and every slot's down vectors are all in flight
+  // before the first product (per slot, the lane still adds its vectors in
+  // increasing order)
+  constexpr int VC = KMAX <= 4 ? 2 : 1;
+  int rowv[KMAX], rsrc[KMAX];
+  float wb[KMAX], dot[KMAX], gw[KMAX];
   float wsum = 0.0f;
 #pragma unroll
   for (int s = 0; s < KMAX; ++s) {
-    gw[s] = 0.0f;
-    if (s >= k) continue;
-    const int row = row_of[n * k + s];
-    const int r = src_row(row);
-    const float w = topk_w[n * k + s];
-    wsum += w;
-    const float wb = round_bf16(w);
-    float dot = 0.0f;
-    for (int v = lane; v < nvec; v += 64) {
+    rowv[s] = -1;
+    rsrc[s] = -1;
+    wb[s] = 0.0f;
+    dot[s] = 0.0f;
+    if (s < k) {
+      rowv[s] = row_of[n * k + s];
+      rsrc[s] = src_row(rowv[s]);
+      const float w = topk_w[n * k + s];
+      wsum += w;
+      wb[s] = round_bf16(w);
+    }
+  }
+  for (int v0 = lane; v0 < nvec; v0 += 64 * VC) {
+    uint4 gv[VC], dv[KMAX][VC];
+#pragma unroll
+    for (int j = 0; j < VC; ++j) {
+      const int v = v0 + 64 * j;
+      gv[j] = v < nvec ? gor[v] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s)
+        dv[s][j] = (rsrc[s] >= 0 && v < nvec)
+                       ? reinterpret_cast<const uint4*>(down + static_cast<int64_t>(rsrc[s]) * D)[v]
+                       : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < VC; ++j) {
+      const int v = v0 + 64 * j;
+      if (v >= nvec) continue;
       float g[8];
-      unpack8(gor[v], g);
-      if (r >= 0) {
-        float d[8];
-        unpack8(reinterpret_cast<const uint4*>(down + static_cast<int64_t>(r) * D)[v], d);
+      unpack8(gv[j], g);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dot += d[i] * g[i];
-      }
-      if (row >= 0) {
-        float o[8];
+      for (int s = 0; s < KMAX; ++s) {
+        if (rsrc[s] >= 0) {
+          float d[8];
+          unpack8(dv[s][j], d);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = g[i] * wb;
-        reinterpret_cast<uint4*>(wgo + static_cast<int64_t>(row) * D)[v] = pack8(o);
+          for (int i = 0; i < 8; ++i) dot[s] += d[i] * g[i];
+        }
+        if (rowv[s] >= 0) {
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = g[i] * wb[s];
+          reinterpret_cast<uint4*>(wgo + static_cast<int64_t>(rowv[s]) * D)[v] = pack8(o);
+        }
       }
     }
-    gw[s] = wave_sum(dot);
   }
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) gw[s] = s < k ? wave_sum(dot[s]) : 0.0f;
   if (capacity_mode && !(wsum > 0.0f)) {
 #pragma unroll
     for (int s = 0; s < KMAX; ++s) gw[s] = 0.0f;
@@ -481,9 +567,26 @@ extern "C" int ffmoe_combine(const void* rows, const int32_t* row_of, const floa
                              const void* addend, int64_t N, int D, int k, void* out, void* stream) {
   if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_combine: D must be a positive multiple of 8");
   if (k < 1 || k > FFMOE_MAX_TOPK) return set_error("ffmoe_combine: bad k");
-  hipLaunchKernelGGL(combine_kernel, dim3(grid_for(N * (D / 8))), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(rows), row_of,
-                     topk_w, static_cast<const bf16_t*>(addend), N, D, k, static_cast<bf16_t*>(out));
+  const int nvec = D / 8;
+  const bool two = nvec % 2 == 0 && k <= 8;  // two vectors per thread
+  const unsigned grid = grid_for(N * (two ? nvec / 2 : nvec));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto rb = static_cast<const bf16_t*>(rows);
+  auto ab = static_cast<const bf16_t*>(addend);
+  auto ob = static_cast<bf16_t*>(out);
+#define FFMOE_CB(KM, U) \
+  hipLaunchKernelGGL((combine_kernel<KM, U>), dim3(grid), dim3(256), 0, st, rb, row_of, topk_w, ab, N, D, k, ob)
+  if (two) {
+    if (k <= 2) FFMOE_CB(2, 2);
+    else if (k <= 4) FFMOE_CB(4, 2);
+    else FFMOE_CB(8, 2);
+  } else {
+    if (k <= 2) FFMOE_CB(2, 1);
+    else if (k <= 4) FFMOE_CB(4, 1);
+    else if (k <= 8) FFMOE_CB(8, 1);
+    else FFMOE_CB(16, 1);
+  }
+#undef FFMOE_CB
   if (check_launch("combine_kernel")) return 1;
   return clear_error();
 }
@@ -512,22 +615,15 @@ extern "C" int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, 
   if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_gate_grad: D must be a positive multiple of 8");
   if (E < 1 || E > FFMOE_MAX_FUSED_GATE_E) return set_error("ffmoe_gate_grad: E out of range");
   const int64_t nchunk = (N + kGateChunk - 1) / kGateChunk;
-  if (nchunk > 65535) return set_error("ffmoe_gate_grad: N too large (at most 4194240 tokens)");
+  if (nchunk > 65535) return set_error("ffmoe_gate_grad: N too large (at most 8388480 tokens)");
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* part = static_cast<float*>(workspace);
-  const dim3 grid(static_cast<unsigned>((D + 255) / 256), static_cast<unsigned>(nchunk));
-  if (E <= 8)
-    hipLaunchKernelGGL(gate_grad_partial_kernel<8>, grid, dim3(256), 0, st,
-                       static_cast<const bf16_t*>(gl), static_cast<const bf16_t*>(x), N, D, E, part);
-  else if (E <= 16)
-    hipLaunchKernelGGL(gate_grad_partial_kernel<16>, grid, dim3(256), 0, st,
-                       static_cast<const bf16_t*>(gl), static_cast<const bf16_t*>(x), N, D, E, part);
-  else
-    hipLaunchKernelGGL(gate_grad_partial_kernel<32>, grid, dim3(256), 0, st,
-                       static_cast<const bf16_t*>(gl), static_cast<const bf16_t*>(x), N, D, E, part);
+  const dim3 grid(static_cast<unsigned>((D + kGateCols - 1) / kGateCols), static_cast<unsigned>(nchunk));
+  hipLaunchKernelGGL(gate_grad_partial_kernel, grid, dim3(256), 0, st, static_cast<const bf16_t*>(gl),
+                     static_cast<const bf16_t*>(x), N, D, E, part);
   if (check_launch("gate_grad_partial_kernel")) return 1;
   const int64_t total = static_cast<int64_t>(E) * D;
-  hipLaunchKernelGGL(gate_grad_final_kernel, dim3(static_cast<unsigned>((total + 63) / 64)),
+  hipLaunchKernelGGL(gate_grad_final_kernel, dim3(static_cast<unsigned>((total / 4 + 15) / 16)),
                      dim3(256), 0, st, part, nchunk, D, E, static_cast<bf16_t*>(dgate));
   if (check_launch("gate_grad_final_kernel")) return 1;
   return clear_error();

@@ -6,6 +6,7 @@
 // bit for bit, and every fp32 reduction has a fixed order.
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "common.h"
 
@@ -358,82 +359,259 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
 
 // Single block: per-expert prefix over route blocks (block bases replace the
 // histogram in place), counts, row offsets, GEMM tile offsets, losses and
-// routing metrics.  The 256 threads are split into E groups of G threads;
-// thread g of expert e owns a contiguous run of route blocks, so the scan is
-// a per-thread sum, a prefix over the G partial sums, then a second pass
-// writing the bases.  Every sum has a fixed order (deterministic).
-__global__ __launch_bounds__(256) void route_scan_kernel(
+// routing metrics.  A thread owns EV adjacent experts (EV = 4 when E % 4 ==
+// 0: 16-byte loads) and a contiguous run of route blocks; consecutive
+// threads take consecutive expert groups of the same run, so the loads of a
+// wave are coalesced.  Each thread keeps kScanBatch loads of each array in
+// flight (the histogram comes from other XCDs' writes, so every load is a
+// long trip), the chunk sums are scanned across the runs in LDS (log2 G
+// steps), then a second pass writes the bases.  Every sum is a fixed tree or
+// sequence (deterministic).
+constexpr int kScanThreads = 1024;
+constexpr int kScanBatch = 8;
+
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+template <int EV, typename T>
+__device__ __forceinline__ void load_ev(const T* p, bool in, T* out) {
+  if constexpr (EV == 4) {
+    using V = typename std::conditional<std::is_same<T, int>::value, int4, float4>::type;
+    const V v = in ? *reinterpret_cast<const V*>(p) : V{0, 0, 0, 0};
+    out[0] = v.x;
+    out[1] = v.y;
+    out[2] = v.z;
+    out[3] = v.w;
+  } else {
+    out[0] = in ? *p : T(0);
+  }
+}
+
+template <int EV, typename T>
+__device__ __forceinline__ void store_lds_ev(T* p, const T* v) {
+  if constexpr (EV == 4) {
+    using V = typename std::conditional<std::is_same<T, int>::value, int4, float4>::type;
+    *reinterpret_cast<V*>(p) = V{v[0], v[1], v[2], v[3]};
+  } else {
+    p[0] = v[0];
+  }
+}
+
+template <int EV>
+__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     int64_t N, int64_t nblk, int E, int k, int mt, int bm, float aux_coeff, float z_coeff,
     int gating, RouteWs ws, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ tile_offsets, float* __restrict__ stats, int32_t* __restrict__ istats,
     float* __restrict__ aux_out, float* __restrict__ z_out) {
-  __shared__ int s_part[256];
-  __shared__ float s_fpart[256];
-  __shared__ float s_z[256];
-  __shared__ int s_rows[FFMOE_MAX_EXPERTS];
-  __shared__ int s_tiles[FFMOE_MAX_EXPERTS];
+  constexpr int kWaves = kScanThreads / kWave;
+  constexpr int kEW = FFMOE_MAX_EXPERTS / kWave;  // waves that hold one expert per lane
+  __shared__ __attribute__((aligned(16))) int s_i[kScanThreads * EV];
+  __shared__ __attribute__((aligned(16))) float s_f[kScanThreads * EV];
+  __shared__ int s_t[FFMOE_MAX_EXPERTS];
   __shared__ int s_cnt[FFMOE_MAX_EXPERTS];
-  __shared__ float s_fp[FFMOE_MAX_EXPERTS];
+  __shared__ float s_p[FFMOE_MAX_EXPERTS];
+  __shared__ float s_zw[kWaves];
+  __shared__ float s_fpw[kEW];
+  __shared__ long long s_totw[kEW];
+  __shared__ int s_dw[kEW], s_mxw[kEW], s_mnw[kEW];
   const int tid = threadIdx.x;
-  const int G = 256 / E;  // threads per expert (E <= 256)
-  const int e = tid / G, g = tid % G;
-  const bool active = e < E;
+  const int EQ = E / EV;  // expert groups
+  // runs of route blocks per group (threads per group): at least a batch of
+  // blocks per run, so the LDS scan over runs stays short
+  const int64_t g_cap = (nblk + kScanBatch - 1) / kScanBatch;
+  const int G = static_cast<int>(min<int64_t>(kScanThreads / EQ, g_cap > 0 ? g_cap : 1));
+  const int eq = tid % EQ, g = tid / EQ;
+  const bool active = g < G;
   const int64_t chunk = (nblk + G - 1) / G;
   const int64_t b0 = active ? min<int64_t>(nblk, g * chunk) : 0;
   const int64_t b1 = active ? min<int64_t>(nblk, b0 + chunk) : 0;
-  int run = 0;
-  float ps = 0.0f;
-  for (int64_t b = b0; b < b1; ++b) {
-    run += ws.hist[b * E + e];
-    ps += (gating == FFMOE_GATING_SOFTMAX) ? ws.psum[b * E + e] : ws.ssum[b * E + e];
+  const float* fsrc = (gating == FFMOE_GATING_SOFTMAX) ? ws.psum : ws.ssum;
+  const int64_t col = static_cast<int64_t>(eq) * EV;
+
+  // the first batch of counts stays in registers for the second pass (one
+  // expert per thread; with four, the registers go to more loads in flight)
+  constexpr bool kKeep = EV == 1;
+  int run[EV];
+  float ps[EV];
+  int first[kScanBatch][EV];
+#pragma unroll
+  for (int v = 0; v < EV; ++v) {
+    run[v] = 0;
+    ps[v] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) first[j][v] = 0;
   }
-  s_part[tid] = run;
-  s_fpart[tid] = ps;
-  // z: strided partial sums, reduced below in thread order
-  float z = 0.0f;
-  for (int64_t b = tid; b < nblk; b += 256) z += ws.zpart[b];
-  s_z[tid] = z;
-  __syncthreads();
-  if (active) {
-    int base = 0;
-    for (int q = 0; q < g; ++q) base += s_part[e * G + q];
-    for (int64_t b = b0; b < b1; ++b) {
-      const int c = ws.hist[b * E + e];
-      ws.hist[b * E + e] = base;
-      base += c;
+  for (int64_t b = b0; b < b1; b += kScanBatch) {
+    int c[kScanBatch][EV];
+    float p[kScanBatch][EV];
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) {
+      const bool in = b + j < b1;
+      load_ev<EV>(ws.hist + (b + j) * E + col, in, c[j]);
+      load_ev<EV>(fsrc + (b + j) * E + col, in, p[j]);
     }
-    if (g == G - 1) {  // base is now the expert's total
-      float P = 0.0f;
-      for (int q = 0; q < G; ++q) P += s_fpart[e * G + q];
-      counts[e] = base;
-      s_cnt[e] = base;
-      const int rows = min(base, mt);
-      s_rows[e] = rows;
-      s_tiles[e] = (rows + bm - 1) / bm;
-      s_fp[e] = (static_cast<float>(base) / static_cast<float>(N)) * (P / static_cast<float>(N));
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) {
+#pragma unroll
+      for (int v = 0; v < EV; ++v) {
+        run[v] += c[j][v];
+        ps[v] += p[j][v];  // in block order; the padding adds +0
+        if (kKeep && b == b0) first[j][v] = c[j][v];
+      }
+    }
+  }
+  // z: strided partial sums, reduced below by a fixed tree
+  float z = 0.0f;
+  for (int64_t b = tid; b < nblk; b += kScanThreads) z += ws.zpart[b];
+
+  // inclusive scan of each expert's chunk sums over the runs (Hillis-Steele;
+  // run g of group eq is thread g * EQ + eq)
+  int incl[EV];
+  float ptot[EV];
+#pragma unroll
+  for (int v = 0; v < EV; ++v) {
+    incl[v] = run[v];
+    ptot[v] = ps[v];
+  }
+  store_lds_ev<EV>(s_i + tid * EV, incl);
+  store_lds_ev<EV>(s_f + tid * EV, ptot);
+  __syncthreads();
+  for (int off = 1; off < G; off <<= 1) {
+    int ai[EV];
+    float af[EV];
+    const bool has = active && g >= off;
+    load_ev<EV>(s_i + (has ? tid - off * EQ : tid) * EV, has, ai);
+    load_ev<EV>(s_f + (has ? tid - off * EQ : tid) * EV, has, af);
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < EV; ++v) {
+      incl[v] += ai[v];
+      ptot[v] += af[v];
+    }
+    store_lds_ev<EV>(s_i + tid * EV, incl);
+    store_lds_ev<EV>(s_f + tid * EV, ptot);
+    __syncthreads();
+  }
+  if (active) {
+    int base[EV];
+#pragma unroll
+    for (int v = 0; v < EV; ++v) base[v] = incl[v] - run[v];
+    for (int64_t b = b0; b < b1; b += kScanBatch) {
+      int c[kScanBatch][EV];
+#pragma unroll
+      for (int j = 0; j < kScanBatch; ++j) {
+        if (kKeep && b == b0) {
+#pragma unroll
+          for (int v = 0; v < EV; ++v) c[j][v] = first[j][v];
+        } else {
+          load_ev<EV>(ws.hist + (b + j) * E + col, b + j < b1, c[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kScanBatch; ++j) {
+        if (b + j < b1) {
+          int32_t* dst = ws.hist + (b + j) * E + col;
+          if constexpr (EV == 4) {
+            *reinterpret_cast<int4*>(dst) = make_int4(base[0], base[1], base[2], base[3]);
+          } else {
+            dst[0] = base[0];
+          }
+#pragma unroll
+          for (int v = 0; v < EV; ++v) base[v] += c[j][v];
+        }
+      }
+    }
+    if (g == G - 1) {  // incl is each expert's total
+#pragma unroll
+      for (int v = 0; v < EV; ++v) {
+        const int e = eq * EV + v;
+        s_cnt[e] = incl[v];
+        s_p[e] = ptot[v];
+        counts[e] = incl[v];
+      }
+    }
+  }
+  __syncthreads();
+
+  // per expert (thread q < E): rows, tiles, the aux term; exclusive scans of
+  // rows and tiles over the experts
+  int cnt = 0, rows = 0, tiles = 0;
+  float fp = 0.0f;
+  if (tid < E) {
+    cnt = s_cnt[tid];
+    rows = min(cnt, mt);
+    tiles = (rows + bm - 1) / bm;
+    fp = (static_cast<float>(cnt) / static_cast<float>(N)) * (s_p[tid] / static_cast<float>(N));
+  }
+  int r_in = rows, t_in = tiles;
+  if (tid < FFMOE_MAX_EXPERTS) {
+    s_i[tid] = rows;
+    s_t[tid] = tiles;
+  }
+  __syncthreads();
+  for (int off = 1; off < E; off <<= 1) {
+    int ar = 0, at = 0;
+    if (tid < E && tid >= off) {
+      ar = s_i[tid - off];
+      at = s_t[tid - off];
+    }
+    __syncthreads();
+    if (tid < E) {
+      r_in += ar;
+      t_in += at;
+      s_i[tid] = r_in;
+      s_t[tid] = t_in;
+    }
+    __syncthreads();
+  }
+  if (tid < E) {
+    offsets[tid] = r_in - rows;
+    tile_offsets[tid] = t_in - tiles;
+    if (tid == E - 1) {
+      offsets[E] = r_in;
+      tile_offsets[E] = t_in;
+    }
+  }
+
+  // fixed-tree reductions: z over all threads, the rest over the experts
+  const int wave = tid / kWave, lane = tid % kWave;
+  const auto add_f = [](float x, float y) { return x + y; };
+  const float zw = wave_reduce(z, add_f);
+  if (lane == 0) s_zw[wave] = zw;
+  if (wave < kEW) {
+    const bool ex = tid < E;
+    const float fpw = wave_reduce(fp, add_f);
+    const long long tw = wave_reduce(static_cast<long long>(cnt),
+                                     [](long long x, long long y) { return x + y; });
+    const int dw = wave_reduce(cnt - rows, [](int x, int y) { return x + y; });
+    const int mxw = wave_reduce(cnt, [](int x, int y) { return max(x, y); });
+    const int mnw = wave_reduce(ex ? cnt : 0x7fffffff, [](int x, int y) { return min(x, y); });
+    if (lane == 0) {
+      s_fpw[wave] = fpw;
+      s_totw[wave] = tw;
+      s_dw[wave] = dw;
+      s_mxw[wave] = mxw;
+      s_mnw[wave] = mnw;
     }
   }
   __syncthreads();
   if (tid == 0) {
-    int ro = 0, to = 0, mx = 0, mn = 0x7fffffff, dropped = 0;
-    int64_t tot = 0;
-    float fp = 0.0f;
-    for (int q = 0; q < E; ++q) {
-      offsets[q] = ro;
-      tile_offsets[q] = to;
-      ro += s_rows[q];
-      to += s_tiles[q];
-      mx = max(mx, s_cnt[q]);
-      mn = min(mn, s_cnt[q]);
-      dropped += s_cnt[q] - s_rows[q];
-      tot += s_cnt[q];
-      fp += s_fp[q];
+    float zt = 0.0f, fpt = 0.0f;
+    for (int q = 0; q < kWaves; ++q) zt += s_zw[q];
+    long long tot = 0;
+    int mx = 0, mn = 0x7fffffff, dropped = 0;
+    for (int q = 0; q < kEW; ++q) {
+      fpt += s_fpw[q];
+      tot += s_totw[q];
+      dropped += s_dw[q];
+      mx = max(mx, s_mxw[q]);
+      mn = min(mn, s_mnw[q]);
     }
-    offsets[E] = ro;
-    tile_offsets[E] = to;
-    float zt = 0.0f;
-    for (int q = 0; q < 256; ++q) zt += s_z[q];
-    stats[FFMOE_STAT_AUX] = aux_coeff * static_cast<float>(E) * fp;
+    stats[FFMOE_STAT_AUX] = aux_coeff * static_cast<float>(E) * fpt;
     stats[FFMOE_STAT_Z] = z_coeff * (zt / static_cast<float>(N));
     if (aux_out != nullptr) *aux_out = stats[FFMOE_STAT_AUX];
     if (z_out != nullptr) *z_out = stats[FFMOE_STAT_Z];
@@ -644,9 +822,15 @@ extern "C" int ffmoe_route_scan(int64_t N, int E, int k, int mt, int gemm_bm, fl
   if (N <= 0 || E < 1 || E > FFMOE_MAX_EXPERTS) return set_error("ffmoe_route_scan: bad N/E");
   if (mt < 0 || gemm_bm <= 0) return set_error("ffmoe_route_scan: bad mt/gemm_bm");
   RouteWs ws = route_ws(workspace, N, E);
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), N,
-                     route_blocks(N), E, k, mt, gemm_bm, aux_coeff, z_coeff, gating, ws, counts,
-                     offsets, tile_offsets, stats, istats, aux_out, z_out);
+  // four experts per thread: 16-byte loads of the per-block arrays
+  if (E % 4 == 0 && reinterpret_cast<uintptr_t>(workspace) % 16 == 0)
+    hipLaunchKernelGGL(route_scan_kernel<4>, dim3(1), dim3(kScanThreads), 0, static_cast<hipStream_t>(stream),
+                       N, route_blocks(N), E, k, mt, gemm_bm, aux_coeff, z_coeff, gating, ws, counts,
+                       offsets, tile_offsets, stats, istats, aux_out, z_out);
+  else
+    hipLaunchKernelGGL(route_scan_kernel<1>, dim3(1), dim3(kScanThreads), 0, static_cast<hipStream_t>(stream),
+                       N, route_blocks(N), E, k, mt, gemm_bm, aux_coeff, z_coeff, gating, ws, counts,
+                       offsets, tile_offsets, stats, istats, aux_out, z_out);
   if (check_launch("route_scan_kernel")) return 1;
   return clear_error();
 }

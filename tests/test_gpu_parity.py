@@ -85,7 +85,8 @@ def test_gate_logits_and_routing(N, D, E):
 
 @pytest.mark.parametrize("N,E,k,mt,cap", [(8192, 8, 2, None, False), (1000, 64, 8, 40, False),
                                            (1000, 64, 8, 40, True), (3, 8, 2, None, False),
-                                           (4096, 256, 8, None, False)])
+                                           (4096, 256, 8, None, False), (777, 7, 3, None, False),
+                                           (2000, 33, 5, 100, True), (16384, 64, 8, None, False)])
 def test_permutation_bit_exact(N, E, k, mt, cap):
     from flashfusedmoe_amd import ops
     D = 128
