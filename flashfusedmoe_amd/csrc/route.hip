@@ -202,15 +202,24 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
   }
   __syncthreads();
 
-  // One thread per token: scores, top-k, weights, logsumexp.
-  if (tid < kRouteTokens) {
-    const int t = tid;
+  // Scores, top-k, weights, logsumexp: four lanes per token (lane 4t + j of
+  // token t takes experts j, j + 4, ... in order).  The lanes' partial
+  // logsumexps, pre-softmax sums and top-k lists are combined by a butterfly
+  // over the four lanes (xor 1, then xor 2): each step adds the same two
+  // operands on both partners, so all four lanes end with identical values,
+  // and the top-k order (value desc, index asc) is total, so the merged list
+  // is the single-pass list.  Lane j == 0 then writes the token's results.
+  {
+    constexpr int LPT = kRouteThreads / kRouteTokens;
+    static_assert(LPT == 4, "four lanes per token");
+    const int t = tid / LPT, jl = tid % LPT;
+    const bool tok_ok = t < ntok;
+    const bf16_t* lr = L + t * LS;
     float lse = 0.0f;
-    if (t < ntok) {
-      const bf16_t* lr = L + t * LS;
-      // logsumexp of the logits (z-loss and the pre-softmax probabilities)
-      float m = -INFINITY, s = 0.0f;
-      for (int e = 0; e < E; ++e) {
+    // logsumexp of the logits (z-loss and the pre-softmax probabilities)
+    float m = -INFINITY, s = 0.0f;
+    if (tok_ok) {
+      for (int e = jl; e < E; e += LPT) {
         const float l = bf16_to_f32(lr[e]);
         if (l > m) {
           s = s * expf(m - l) + 1.0f;
@@ -219,24 +228,39 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
           s += expf(l - m);
         }
       }
-      lse = m + logf(s);
-      float psum = 0.0f;  // pre-softmax: sum of exp(l - max) in expert order
-      if (o.pre_softmax)
-        for (int e = 0; e < E; ++e) psum += expf(bf16_to_f32(lr[e]) - m);
-      // selection score of expert e (fused_moe.py:144-200)
-      auto score = [&](int e) {
-        const float l = bf16_to_f32(lr[e]);
-        float sc;
-        if (gating == FFMOE_GATING_SOFTMAX)
-          sc = o.pre_softmax ? expf(l - m) / psum : l;
-        else
-          sc = 1.0f / (1.0f + expf(-l));
-        if (o.bias != nullptr) sc = o.bias_round ? round_bf16(sc + o.bias[e]) : sc + o.bias[e];
-        return sc;
-      };
-      TopK<KMAX> tk;
-      tk.init();
-      if (o.n_group > 0) {
+    }
+#pragma unroll
+    for (int off = 1; off < LPT; off <<= 1) {
+      const float m2 = __shfl_xor(m, off, kWave), s2 = __shfl_xor(s, off, kWave);
+      const float mn = fmaxf(m, m2);
+      const float a1 = m == -INFINITY ? 0.0f : s * expf(m - mn);
+      const float a2 = m2 == -INFINITY ? 0.0f : s2 * expf(m2 - mn);
+      s = a1 + a2;
+      m = mn;
+    }
+    if (tok_ok) lse = m + logf(s);
+    float psum = 0.0f;  // pre-softmax: sum of exp(l - max)
+    if (o.pre_softmax) {
+      if (tok_ok)
+        for (int e = jl; e < E; e += LPT) psum += expf(bf16_to_f32(lr[e]) - m);
+#pragma unroll
+      for (int off = 1; off < LPT; off <<= 1) psum += __shfl_xor(psum, off, kWave);
+    }
+    // selection score of expert e (fused_moe.py:144-200)
+    auto score = [&](int e) {
+      const float l = bf16_to_f32(lr[e]);
+      float sc;
+      if (gating == FFMOE_GATING_SOFTMAX)
+        sc = o.pre_softmax ? expf(l - m) / psum : l;
+      else
+        sc = 1.0f / (1.0f + expf(-l));
+      if (o.bias != nullptr) sc = o.bias_round ? round_bf16(sc + o.bias[e]) : sc + o.bias[e];
+      return sc;
+    };
+    TopK<KMAX> tk;
+    tk.init();
+    if (o.n_group > 0) {
+      if (tok_ok && jl == 0) {
         // group-limited top-k (fused_moe.py:203-251): groups ranked by the sum
         // of their best top_k/topk_group scores (or their best score), the
         // best topk_group groups kept, top_k taken among their experts
@@ -273,9 +297,25 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
           const int g = e / epg;
           if (keep[g >> 5] >> (g & 31) & 1u) tk.push(score(e), e, k);
         }
-      } else {
-        for (int e = 0; e < E; ++e) tk.push(score(e), e, k);
       }
+    } else {
+      if (tok_ok)
+        for (int e = jl; e < E; e += LPT) tk.push(score(e), e, k);
+#pragma unroll
+      for (int off = 1; off < LPT; off <<= 1) {
+        float pv[KMAX];
+        int pi[KMAX];
+#pragma unroll
+        for (int q = 0; q < KMAX; ++q) {
+          pv[q] = __shfl_xor(tk.v[q], off, kWave);
+          pi[q] = __shfl_xor(tk.i[q], off, kWave);
+        }
+#pragma unroll
+        for (int q = 0; q < KMAX; ++q)
+          if (q < k && pi[q] >= 0) tk.push(pv[q], pi[q], k);
+      }
+    }
+    if (tok_ok && jl == 0) {
       float w[KMAX];
       float wsum = 0.0f;
       if (gating == FFMOE_GATING_SOFTMAX && !o.pre_softmax) {
@@ -326,24 +366,40 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
       }
       if (lse_out != nullptr) lse_out[n] = lse;
     }
-    zl[t] = (t < ntok) ? lse * lse : 0.0f;
+    if (jl == 0) zl[t] = tok_ok ? lse * lse : 0.0f;
   }
   __syncthreads();
 
-  // One thread per expert: block-local stable ranks (ascending j), counts,
-  // weight sums and sigmoid sums, all in a fixed order.
+  // Block-local stable ranks (ascending j), counts, weight sums and sigmoid
+  // sums, all in a fixed order: thread q owns experts q, q + 64, ... and
+  // makes one pass over the block's entries for all of them.
+  constexpr int EPT = (ET * 16 + kRouteThreads - 1) / kRouteThreads;
   const int nent = ntok * k;
-  for (int e = tid; e < E; e += kRouteThreads) {
-    int cnt = 0;
-    float ps = 0.0f;
-    for (int j = 0; j < nent; ++j) {
-      if (sel_i[j] == e) {
-        rank_local[tok_base * k + j] = cnt++;
-        ps += sel_w[j];
+  int cnt[EPT];
+  float ps[EPT];
+#pragma unroll
+  for (int v = 0; v < EPT; ++v) {
+    cnt[v] = 0;
+    ps[v] = 0.0f;
+  }
+#pragma unroll 4
+  for (int j = 0; j < nent; ++j) {
+    const int ej = sel_i[j];
+    const float wj = sel_w[j];
+#pragma unroll
+    for (int v = 0; v < EPT; ++v) {
+      if (ej == tid + v * kRouteThreads) {
+        rank_local[tok_base * k + j] = cnt[v]++;
+        ps[v] += wj;
       }
     }
-    ws.hist[blk * E + e] = cnt;
-    ws.psum[blk * E + e] = ps;
+  }
+#pragma unroll
+  for (int v = 0; v < EPT; ++v) {
+    const int e = tid + v * kRouteThreads;
+    if (e >= E) continue;
+    ws.hist[blk * E + e] = cnt[v];
+    ws.psum[blk * E + e] = ps[v];
     if (need_ssum) {
       float ss = 0.0f;
       for (int t = 0; t < ntok; ++t) ss += 1.0f / (1.0f + expf(-bf16_to_f32(L[t * LS + e])));
