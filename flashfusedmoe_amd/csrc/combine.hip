@@ -86,36 +86,78 @@ __global__ __launch_bounds__(256) void combine_kernel(const bf16_t* __restrict__
 //   out[n] = bf16(bf16(sum_s ghb[src(row_of[n*k+s])]) + bf16(gl[n,:] . gate))
 // The sum over slots is fp32 in slot order (moe_ops.py:156-241 with unit
 // weights, fused_moe.py:556-561); the gl . gate product is fp32 over experts
-// in index order, rounded to bf16 as the reference's bf16 `gl @ gate` GEMM
-// output is (fused_moe.py:590).
+// in index order, two experts per v_dot2c_f32_bf16 (each bf16 product is
+// exact in fp32), rounded to bf16 as the reference's bf16 `gl @ gate` GEMM
+// output is (fused_moe.py:590).  The slot rows are gathered with all their
+// loads in flight, the gate rows (L2-resident) four expert pairs at a time.
+template <int KMAX>
 __global__ __launch_bounds__(256) void dx_reduce_kernel(const bf16_t* __restrict__ rows,
                                                         const int32_t* __restrict__ row_of,
                                                         const bf16_t* __restrict__ gl,
                                                         const bf16_t* __restrict__ gate, int64_t N,
                                                         int D, int E, int k,
                                                         bf16_t* __restrict__ out) {
+  constexpr int PB = 4;  // expert pairs per batch of loads
   const int nvec = D / 8;
   const int64_t total = N * nvec;
+  const int EP = E / 2;
   for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
        u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t n = u / nvec;
     const int v = static_cast<int>(u % nvec);
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < k; ++s) {
-      const int r = src_row(row_of[n * k + s]);
-      if (r < 0) continue;
-      float f[8];
-      unpack8(reinterpret_cast<const uint4*>(rows + static_cast<int64_t>(r) * D)[v], f);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += f[i];
-    }
+    int r[KMAX];
+    uint4 val[KMAX][1];
+    gather_rows<KMAX, 1>(rows, row_of, n, k, nvec, v, 0, r, val);
     float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int e = 0; e < E; ++e) {
-      const float g = bf16_to_f32(gl[n * E + e]);
+    for (int p0 = 0; p0 < EP; p0 += PB) {
+      uint32_t gp[PB];
+      uint4 g0[PB], g1[PB];
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        const int pr = p0 + q;
+        const bool ok = pr < EP;
+        // with an even E, pair pr of gl row n is 4-byte aligned
+        const bf16_t* gpp = gl + n * E + 2 * pr;
+        gp[q] = !ok ? 0u
+                    : (E & 1) ? (static_cast<uint32_t>(gpp[0]) | (static_cast<uint32_t>(gpp[1]) << 16))
+                              : *reinterpret_cast<const uint32_t*>(gpp);
+        g0[q] = ok ? reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(2 * pr) * D)[v]
+                   : make_uint4(0, 0, 0, 0);
+        g1[q] = ok ? reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(2 * pr + 1) * D)[v]
+                   : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        if (p0 + q >= EP) break;
+        const bf16x2_t gv = __builtin_bit_cast(bf16x2_t, gp[q]);
+        const uint32_t w0[4] = {g0[q].x, g0[q].y, g0[q].z, g0[q].w};
+        const uint32_t w1[4] = {g1[q].x, g1[q].y, g1[q].z, g1[q].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // columns 2j, 2j+1 of experts 2pr (low half) and 2pr+1 (high half)
+          const uint32_t lo = (w0[j] & 0xffffu) | (w1[j] << 16);
+          const uint32_t hi = (w0[j] >> 16) | (w1[j] & 0xffff0000u);
+          a[2 * j] = __builtin_amdgcn_fdot2_f32_bf16(gv, __builtin_bit_cast(bf16x2_t, lo), a[2 * j], false);
+          a[2 * j + 1] =
+              __builtin_amdgcn_fdot2_f32_bf16(gv, __builtin_bit_cast(bf16x2_t, hi), a[2 * j + 1], false);
+        }
+      }
+    }
+    if (E & 1) {  // the last expert of an odd count
+      const float g = bf16_to_f32(gl[n * E + E - 1]);
       float w[8];
-      unpack8(reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(e) * D)[v], w);
+      unpack8(reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(E - 1) * D)[v], w);
 #pragma unroll
       for (int i = 0; i < 8; ++i) a[i] += g * w[i];
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+      if (r[s] < 0) continue;
+      float f[8];
+      unpack8(val[s][0], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += f[i];
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = round_bf16(acc[i]) + round_bf16(a[i]);
@@ -597,10 +639,19 @@ extern "C" int ffmoe_dx_reduce(const void* ghb, const int32_t* row_of, const voi
   if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_dx_reduce: D must be a positive multiple of 8");
   if (k < 1 || k > FFMOE_MAX_TOPK) return set_error("ffmoe_dx_reduce: bad k");
   if (E < 1 || E > FFMOE_MAX_FUSED_GATE_E) return set_error("ffmoe_dx_reduce: E out of range");
-  hipLaunchKernelGGL(dx_reduce_kernel, dim3(grid_for(N * (D / 8))), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(ghb), row_of,
-                     static_cast<const bf16_t*>(gl), static_cast<const bf16_t*>(gate), N, D, E, k,
-                     static_cast<bf16_t*>(out));
+  const dim3 grid(grid_for(N * (D / 8)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto rb = static_cast<const bf16_t*>(ghb);
+  auto gb = static_cast<const bf16_t*>(gl);
+  auto wb = static_cast<const bf16_t*>(gate);
+  auto ob = static_cast<bf16_t*>(out);
+#define FFMOE_DX(KM) \
+  hipLaunchKernelGGL((dx_reduce_kernel<KM>), grid, dim3(256), 0, st, rb, row_of, gb, wb, N, D, E, k, ob)
+  if (k <= 2) FFMOE_DX(2);
+  else if (k <= 4) FFMOE_DX(4);
+  else if (k <= 8) FFMOE_DX(8);
+  else FFMOE_DX(16);
+#undef FFMOE_DX
   if (check_launch("dx_reduce_kernel")) return 1;
   return clear_error();
 }
