@@ -168,9 +168,9 @@ __global__ __launch_bounds__(256) void dx_reduce_kernel(const bf16_t* __restrict
 // Gate weight gradient dgate[E, D] = gl^T x (fused_moe.py:591), E <=
 // FFMOE_MAX_FUSED_GATE_E.  Pass 1: a block takes a kGateCols-column slice of
 // kGateChunk tokens.  Thread (row group rg, vector cv) owns 8 columns and the
-// tokens rg, rg + 16, ...: its x loads and gl-row loads are all issued at
-// once (the block's 32 KiB x tile is in flight together, two blocks per CU).
-// Per batch of 8 experts the 16 row groups are added in row-group order
+// tokens rg, rg + 16, ...: its x loads are all issued at once (the block's
+// 32 KiB x tile is in flight together, two blocks per CU), its gl loads per
+// batch of 8 experts.  Per batch the 16 row groups are added in row-group order
 // through LDS into one fp32 partial per block.  Pass 2 sums the partials in
 // a fixed order and rounds to bf16.  x is read once; deterministic.
 constexpr int kGateChunk = 128;
@@ -178,20 +178,14 @@ constexpr int kGateCols = 128;
 constexpr int kGateGroups = 256 / (kGateCols / 8);  // row groups per block
 constexpr int kGateTok = kGateChunk / kGateGroups;  // tokens per thread
 
-__device__ __forceinline__ void gate_gl_row(const bf16_t* __restrict__ gl, int64_t n, int E, int eb,
-                                            bool ok, uint4& packed, float* g) {
-  if ((E & 7) == 0) {
-    packed = ok ? *reinterpret_cast<const uint4*>(gl + n * E + eb) : make_uint4(0, 0, 0, 0);
-  } else {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) g[q] = (ok && eb + q < E) ? bf16_to_f32(gl[n * E + eb + q]) : 0.0f;
-  }
-}
-
+// GL8: E is a multiple of 8 (each batch of 8 experts of a gl row is one
+// aligned 16-byte load and the product runs on bf16 dot2 over token pairs).
+template <bool GL8>
 __global__ __launch_bounds__(256) void gate_grad_partial_kernel(const bf16_t* __restrict__ gl,
                                                                 const bf16_t* __restrict__ x,
                                                                 int64_t N, int D, int E,
                                                                 float* __restrict__ part) {
+  static_assert(kGateTok % 2 == 0, "token pairs");
   __shared__ float4 s_red[kGateGroups][8][kGateCols / 4];
   const int tid = threadIdx.x;
   const int rg = tid / (kGateCols / 8), cv = tid % (kGateCols / 8);
@@ -209,27 +203,53 @@ __global__ __launch_bounds__(256) void gate_grad_partial_kernel(const bf16_t* __
                                : make_uint4(0, 0, 0, 0);
   }
   for (int eb = 0; eb < E; eb += 8) {
-    uint4 gp[kGateTok];
-    float gf[kGateTok][8];
-#pragma unroll
-    for (int j = 0; j < kGateTok; ++j) {
-      const int t = rg + j * kGateGroups;
-      gate_gl_row(gl, n0 + t, E, eb, t < nt, gp[j], gf[j]);
-    }
     float acc[8][8];
 #pragma unroll
     for (int q = 0; q < 8; ++q)
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[q][i] = 0.0f;
+    if constexpr (GL8) {
+      uint4 gp[kGateTok];
 #pragma unroll
-    for (int j = 0; j < kGateTok; ++j) {
-      float xf[8];
-      unpack8(xv[j], xf);
-      if ((E & 7) == 0) unpack8(gp[j], gf[j]);
+      for (int j = 0; j < kGateTok; ++j) {
+        const int t = rg + j * kGateGroups;
+        gp[j] = t < nt ? *reinterpret_cast<const uint4*>(gl + (n0 + t) * E + eb) : make_uint4(0, 0, 0, 0);
+      }
+      // two tokens per v_dot2c_f32_bf16: (gl[t][e], gl[t'][e]) . (x[t][c], x[t'][c]),
+      // each bf16 product exact in fp32; tokens past the chunk hold zeros
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
+      for (int j = 0; j < kGateTok; j += 2) {
+        const uint32_t x0[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        const uint32_t x1[4] = {xv[j + 1].x, xv[j + 1].y, xv[j + 1].z, xv[j + 1].w};
+        const uint32_t g0[4] = {gp[j].x, gp[j].y, gp[j].z, gp[j].w};
+        const uint32_t g1[4] = {gp[j + 1].x, gp[j + 1].y, gp[j + 1].z, gp[j + 1].w};
+        bf16x2_t xp[8], gq[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[q][i] += gf[j][q] * xf[i];
+        for (int w = 0; w < 4; ++w) {
+          xp[2 * w] = __builtin_bit_cast(bf16x2_t, (x0[w] & 0xffffu) | (x1[w] << 16));
+          xp[2 * w + 1] = __builtin_bit_cast(bf16x2_t, (x0[w] >> 16) | (x1[w] & 0xffff0000u));
+          gq[2 * w] = __builtin_bit_cast(bf16x2_t, (g0[w] & 0xffffu) | (g1[w] << 16));
+          gq[2 * w + 1] = __builtin_bit_cast(bf16x2_t, (g0[w] >> 16) | (g1[w] & 0xffff0000u));
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[q][i] = __builtin_amdgcn_fdot2_f32_bf16(gq[q], xp[i], acc[q][i], false);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kGateTok; ++j) {
+        const int t = rg + j * kGateGroups;
+        float g[8], xf[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          g[q] = (t < nt && eb + q < E) ? bf16_to_f32(gl[(n0 + t) * E + eb + q]) : 0.0f;
+        unpack8(xv[j], xf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[q][i] += g[q] * xf[i];
+      }
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -670,8 +690,12 @@ extern "C" int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* part = static_cast<float*>(workspace);
   const dim3 grid(static_cast<unsigned>((D + kGateCols - 1) / kGateCols), static_cast<unsigned>(nchunk));
-  hipLaunchKernelGGL(gate_grad_partial_kernel, grid, dim3(256), 0, st, static_cast<const bf16_t*>(gl),
-                     static_cast<const bf16_t*>(x), N, D, E, part);
+  if (E % 8 == 0)
+    hipLaunchKernelGGL(gate_grad_partial_kernel<true>, grid, dim3(256), 0, st, static_cast<const bf16_t*>(gl),
+                       static_cast<const bf16_t*>(x), N, D, E, part);
+  else
+    hipLaunchKernelGGL(gate_grad_partial_kernel<false>, grid, dim3(256), 0, st, static_cast<const bf16_t*>(gl),
+                       static_cast<const bf16_t*>(x), N, D, E, part);
   if (check_launch("gate_grad_partial_kernel")) return 1;
   const int64_t total = static_cast<int64_t>(E) * D;
   hipLaunchKernelGGL(gate_grad_final_kernel, dim3(static_cast<unsigned>((total / 4 + 15) / 16)),
