@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
-Workload (the reference README's Quick Start layer):
+Workload (configuration C2, the reference README's Quick Start layer):
 fused_moe forward + backward, N = 8192 tokens (B=4, T=2048), D = 1024,
 ffn_dim = 4096 (H = 2048), E = 8, top_k = 2, swiglu, softmax gating,
 aux_loss_coeff = 0.01, z_loss_coeff = 1e-3, bf16.  Synthetic inputs from a
