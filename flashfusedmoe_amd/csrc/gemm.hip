@@ -939,11 +939,24 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
 // One block per tile.
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
-  const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
-  if (tile >= p.total_tiles) return;
   TileCoord tc;
-  if constexpr (MODE == 0) tc = decode_rows_tile<BM, BN>(p, tile, p.m_tiles);
-  else tc = decode_k_tile<BM, BN>(p, tile);
+  if constexpr (MODE == 0) {
+    // Blocks are dispatched round-robin over the 8 XCDs (XCD x runs blocks
+    // x, x + 8, ...).  The grid covers an upper bound of row tiles; the R
+    // real ones (known on the device) are split evenly, each XCD taking a
+    // contiguous run, so no XCD runs a round more than the others.
+    const int R = ld_const(p.tile_offsets, p.E);
+    const int64_t T = static_cast<int64_t>(R) * p.n_tiles;
+    const int64_t per = (T + 7) / 8;
+    const int64_t idx = blockIdx.x >> 3;
+    const int64_t tile = (blockIdx.x & 7) * per + idx;
+    if (idx >= per || tile >= T) return;
+    tc = decode_rows_tile<BM, BN>(p, tile, R);
+  } else {
+    const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
+    if (tile >= p.total_tiles) return;
+    tc = decode_k_tile<BM, BN>(p, tile);
+  }
   if (!tc.valid) return;
   gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
 }
