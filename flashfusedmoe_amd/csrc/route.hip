@@ -371,39 +371,60 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
   __syncthreads();
 
   // Block-local stable ranks (ascending j), counts, weight sums and sigmoid
-  // sums, all in a fixed order: thread q owns experts q, q + 64, ... and
+  // sums, all in a fixed order.  With at most 16 experts and one entry per
+  // lane, one ballot per expert gives every entry its rank (the set lanes
+  // below it) and lane e the mask of expert e's entries, whose weights it
+  // adds in ascending j.  Otherwise thread q owns experts q, q + 64, ... and
   // makes one pass over the block's entries for all of them.
-  constexpr int EPT = (ET * 16 + kRouteThreads - 1) / kRouteThreads;
   const int nent = ntok * k;
-  int cnt[EPT];
-  float ps[EPT];
-#pragma unroll
-  for (int v = 0; v < EPT; ++v) {
-    cnt[v] = 0;
-    ps[v] = 0.0f;
-  }
-#pragma unroll 4
-  for (int j = 0; j < nent; ++j) {
-    const int ej = sel_i[j];
-    const float wj = sel_w[j];
-#pragma unroll
-    for (int v = 0; v < EPT; ++v) {
-      if (ej == tid + v * kRouteThreads) {
-        rank_local[tok_base * k + j] = cnt[v]++;
-        ps[v] += wj;
-      }
-    }
-  }
-#pragma unroll
-  for (int v = 0; v < EPT; ++v) {
-    const int e = tid + v * kRouteThreads;
-    if (e >= E) continue;
-    ws.hist[blk * E + e] = cnt[v];
-    ws.psum[blk * E + e] = ps[v];
+  auto block_sums = [&](int e, int cnt, float ps) {
+    ws.hist[blk * E + e] = cnt;
+    ws.psum[blk * E + e] = ps;
     if (need_ssum) {
       float ss = 0.0f;
       for (int t = 0; t < ntok; ++t) ss += 1.0f / (1.0f + expf(-bf16_to_f32(L[t * LS + e])));
       ws.ssum[blk * E + e] = ss;
+    }
+  };
+  if (ET == 1 && nent <= kRouteThreads) {
+    const int j = tid;
+    const int ej = j < nent ? sel_i[j] : -1;
+    uint64_t mine = 0;
+    for (int e = 0; e < E; ++e) {
+      const uint64_t m = __ballot(ej == e);
+      if (ej == e) rank_local[tok_base * k + j] = __popcll(m & ((1ull << j) - 1));
+      if (tid == e) mine = m;
+    }
+    if (tid < E) {
+      float ps = 0.0f;
+      for (uint64_t m = mine; m != 0; m &= m - 1) ps += sel_w[__builtin_ctzll(m)];
+      block_sums(tid, __popcll(mine), ps);
+    }
+  } else {
+    constexpr int EPT = (ET * 16 + kRouteThreads - 1) / kRouteThreads;
+    int cnt[EPT];
+    float ps[EPT];
+#pragma unroll
+    for (int v = 0; v < EPT; ++v) {
+      cnt[v] = 0;
+      ps[v] = 0.0f;
+    }
+#pragma unroll 4
+    for (int j = 0; j < nent; ++j) {
+      const int ej = sel_i[j];
+      const float wj = sel_w[j];
+#pragma unroll
+      for (int v = 0; v < EPT; ++v) {
+        if (ej == tid + v * kRouteThreads) {
+          rank_local[tok_base * k + j] = cnt[v]++;
+          ps[v] += wj;
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < EPT; ++v) {
+      const int e = tid + v * kRouteThreads;
+      if (e < E) block_sums(e, cnt[v], ps[v]);
     }
   }
   if (tid == 0) {
