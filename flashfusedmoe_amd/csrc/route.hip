@@ -488,7 +488,7 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
   constexpr int kEW = FFMOE_MAX_EXPERTS / kWave;  // waves that hold one expert per lane
   __shared__ __attribute__((aligned(16))) int s_i[kScanThreads * EV];
   __shared__ __attribute__((aligned(16))) float s_f[kScanThreads * EV];
-  __shared__ int s_t[FFMOE_MAX_EXPERTS];
+  __shared__ int s_rw[kEW], s_tw[kEW];
   __shared__ int s_cnt[FFMOE_MAX_EXPERTS];
   __shared__ float s_p[FFMOE_MAX_EXPERTS];
   __shared__ float s_zw[kWaves];
@@ -624,38 +624,26 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     tiles = (rows + bm - 1) / bm;
     fp = (static_cast<float>(cnt) / static_cast<float>(N)) * (s_p[tid] / static_cast<float>(N));
   }
+  // inclusive scans of rows and tiles within each expert wave (shuffles);
+  // the waves' totals are added below through LDS
+  const int wave = tid / kWave, lane = tid % kWave;
   int r_in = rows, t_in = tiles;
-  if (tid < FFMOE_MAX_EXPERTS) {
-    s_i[tid] = rows;
-    s_t[tid] = tiles;
-  }
-  __syncthreads();
-  for (int off = 1; off < E; off <<= 1) {
-    int ar = 0, at = 0;
-    if (tid < E && tid >= off) {
-      ar = s_i[tid - off];
-      at = s_t[tid - off];
+  if (wave < kEW) {
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int ar = __shfl_up(r_in, off, kWave), at = __shfl_up(t_in, off, kWave);
+      if (lane >= off) {
+        r_in += ar;
+        t_in += at;
+      }
     }
-    __syncthreads();
-    if (tid < E) {
-      r_in += ar;
-      t_in += at;
-      s_i[tid] = r_in;
-      s_t[tid] = t_in;
-    }
-    __syncthreads();
-  }
-  if (tid < E) {
-    offsets[tid] = r_in - rows;
-    tile_offsets[tid] = t_in - tiles;
-    if (tid == E - 1) {
-      offsets[E] = r_in;
-      tile_offsets[E] = t_in;
+    if (lane == kWave - 1) {
+      s_rw[wave] = r_in;
+      s_tw[wave] = t_in;
     }
   }
 
   // fixed-tree reductions: z over all threads, the rest over the experts
-  const int wave = tid / kWave, lane = tid % kWave;
   const auto add_f = [](float x, float y) { return x + y; };
   const float zw = wave_reduce(z, add_f);
   if (lane == 0) s_zw[wave] = zw;
@@ -676,6 +664,18 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     }
   }
   __syncthreads();
+  if (tid < E) {
+    for (int w = 0; w < wave; ++w) {
+      r_in += s_rw[w];
+      t_in += s_tw[w];
+    }
+    offsets[tid] = r_in - rows;
+    tile_offsets[tid] = t_in - tiles;
+    if (tid == E - 1) {
+      offsets[E] = r_in;
+      tile_offsets[E] = t_in;
+    }
+  }
   if (tid == 0) {
     float zt = 0.0f, fpt = 0.0f;
     for (int q = 0; q < kWaves; ++q) zt += s_zw[q];
