@@ -58,6 +58,7 @@ struct GemmArgs {
   int act;
   float* part;  // persistent kernel: fp32 partial tiles, one slot per block
   int* flags;   // persistent kernel: one flag per block + an error word
+  int lpt;      // wgrad: test the routing skew and balance the tiles over the XCDs
 };
 
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
@@ -936,6 +937,8 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   __syncthreads();  // the C tile is read before a next tile's loads refill the LDS
 }
 
+constexpr int kLptMaxE = 1024;  // experts the skew-balanced wgrad order handles
+
 // One block per tile.
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
@@ -953,9 +956,66 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
     if (idx >= per || tile >= T) return;
     tc = decode_rows_tile<BM, BN>(p, tile, R);
   } else {
-    const int64_t tile = xcd_remap(blockIdx.x, gridDim.x);
-    if (tile >= p.total_tiles) return;
-    tc = decode_k_tile<BM, BN>(p, tile);
+    // Off the skewed path each XCD takes a contiguous run of tiles (block
+    // x + 8 s runs on XCD x), so neighbouring tiles share its L2.
+    const int64_t per = (p.total_tiles + 7) / 8;
+    const int64_t idx = blockIdx.x >> 3;
+    const int64_t tile = (blockIdx.x & 7) * per + idx;
+    const bool in_run = idx < per && tile < p.total_tiles;
+    if (in_run) tc = decode_k_tile<BM, BN>(p, tile);
+    bool skewed = false;
+    if (p.lpt) {
+      // An expert's tiles all take K = its row count, so when one expert
+      // holds at least 1.5x the mean row count, the XCD holding its tiles
+      // sets the launch time.  Every wave reads the counts and takes the
+      // same decision (one ballot), so the test needs no block barrier.
+      // Loads go out four per lane at a time (clamped in range) before any
+      // is waited for.
+      const int64_t total3 = 3 * static_cast<int64_t>(p.offsets[p.E] - p.offsets[0]);
+      bool heavy = false;
+      for (int i0 = threadIdx.x & 63; i0 < p.E; i0 += 256) {
+        int lo[4], hi[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = min(i0 + 64 * u, p.E - 1);
+          lo[u] = p.offsets[i];
+          hi[u] = p.offsets[i + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          heavy |= i0 + 64 * u < p.E && 2 * static_cast<int64_t>(hi[u] - lo[u]) * p.E >= total3;
+      }
+      skewed = __ballot(heavy && total3 > 0) != 0;
+    }
+    if (skewed) {
+      // Every XCD takes a contiguous slice of ceil(per_e / 8) tiles of every
+      // expert, and the experts are visited heaviest first (ties: lower
+      // index first), so the long tiles start at once and the short ones
+      // fill in behind them.
+      __shared__ int s_cnt[kLptMaxE];
+      __shared__ int s_sel;
+      const int per_e = p.m_tiles * p.n_tiles;
+      const int c = (per_e + 7) / 8;
+      const int sl = static_cast<int>(blockIdx.x >> 3);
+      const int r = sl / c;                                           // rank of the expert
+      const int sub = static_cast<int>(blockIdx.x & 7) * c + sl % c;  // its tile
+      if (r >= p.E || sub >= per_e) return;
+      for (int i = threadIdx.x; i < p.E; i += kThreads) s_cnt[i] = p.offsets[i + 1] - p.offsets[i];
+      __syncthreads();
+      for (int i = threadIdx.x; i < p.E; i += kThreads) {
+        const int ci = s_cnt[i];
+        int rank = 0;
+        for (int j = 0; j < p.E; ++j) {
+          const int cj = s_cnt[j];
+          rank += (cj > ci) || (cj == ci && j < i);
+        }
+        if (rank == r) s_sel = i;
+      }
+      __syncthreads();
+      tc = decode_k_tile<BM, BN>(p, static_cast<int64_t>(s_sel) * per_e + sub);
+    } else if (!in_run) {
+      return;
+    }
   }
   if (!tc.valid) return;
   gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
@@ -1030,11 +1090,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs p) {
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
 static int launch(const GemmArgs& a, hipStream_t st, const char* name) {
   if (a.total_tiles <= 0) return clear_error();
-  const int64_t grid = (a.total_tiles + 7) / 8 * 8;
-  if (grid > 0x7fffffff) return set_error(std::string(name) + ": problem too large");
   // the direct-to-LDS pipeline needs whole K steps (grouped-rows mode) and the
   // transpose-read path; everything else takes the register-staged kernel
   const bool dl = g_use_tr && (MODE == 1 || a.K % DL_BK == 0);
+  const int64_t grid = (dl && a.lpt) ? static_cast<int64_t>(a.E) * 8 * ((a.m_tiles * a.n_tiles + 7) / 8)
+                                     : (a.total_tiles + 7) / 8 * 8;
+  if (grid > 0x7fffffff) return set_error(std::string(name) + ": problem too large");
   if (dl)
     hipLaunchKernelGGL((gemm_dl_kernel<BM, BN, A_KC, B_KC, MODE, EPI>),
                        dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, st, a);
@@ -1222,6 +1283,11 @@ extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t
                                            "gemm_dgrad");
 }
 
+#ifndef FFMOE_WGRAD_LPT_MIN_E
+#define FFMOE_WGRAD_LPT_MIN_E 2
+#endif
+static int wgrad_lpt(int E) { return E >= FFMOE_WGRAD_LPT_MIN_E && E <= kLptMaxE; }
+
 extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
                                 int Nc, void* c_out, void* stream) {
   if (E < 1 || M <= 0 || M % 8 != 0 || Nc <= 0 || Nc % 8 != 0)
@@ -1242,5 +1308,6 @@ extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* o
   a.m_tiles = (M + BM - 1) / BM;
   a.n_tiles = (Nc + BN - 1) / BN;
   a.total_tiles = static_cast<int64_t>(E) * a.m_tiles * a.n_tiles;
+  a.lpt = wgrad_lpt(E);
   return launch<BM, BN, false, false, 1, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_wgrad");
 }

@@ -309,6 +309,49 @@ def test_transpose_and_elementwise_lds_reads_agree(_lib):
     assert torch.equal(res[0], res[1])
 
 
+@pytest.mark.parametrize("E,seed", [(80, 0), (300, 1)])
+def test_wgrad_skewed_counts_against_fp32(E, seed, _lib):
+    """One expert far above the mean row count (plus ties and empty experts)
+    sends the wgrad launch down its heaviest-first, XCD-sliced tile order.
+    Every expert still matches an fp32 product, empty experts are zero, and
+    the heavy expert's tiles are bit-identical to a launch of that expert
+    alone (the order changes which block runs a tile, not its arithmetic)."""
+    L = _lib
+    rng = np.random.default_rng(seed)
+    sizes = rng.integers(0, 48, E)
+    sizes[:6] = 17
+    sizes[6:10] = 0
+    heavy = int(rng.integers(10, E))
+    sizes[heavy] = 3000
+    assert 2 * sizes.max() * E >= 3 * sizes.sum()
+    M, Nc = 264, 520  # partial edge tiles on both sides
+    T = int(sizes.sum())
+    off = np.zeros(E + 1, dtype=np.int32)
+    off[1:] = np.cumsum(sizes)
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(T, M, generator=g).to(torch.bfloat16).cuda()
+    b = torch.randn(T, Nc, generator=g).to(torch.bfloat16).cuda()
+    off_g = torch.from_numpy(off).cuda()
+    c = torch.full((E, M, Nc), float("nan"), dtype=torch.bfloat16, device="cuda")
+    L.call("ffmoe_gemm_wgrad", a.data_ptr(), b.data_ptr(), off_g.data_ptr(), E, M, Nc, c.data_ptr(),
+           L.stream_ptr())
+    ref = torch.zeros(E, M, Nc, device="cuda")
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi > lo:
+            ref[e] = a[lo:hi].float().t() @ b[lo:hi].float()
+    torch.cuda.synchronize()
+    check_close(c, ref, "dW (skewed counts)")
+    assert c[torch.from_numpy(sizes == 0).cuda()].abs().max().item() == 0
+    lo, hi = int(off[heavy]), int(off[heavy + 1])
+    one_off = torch.tensor([0, hi - lo], dtype=torch.int32, device="cuda")
+    c1 = torch.empty(1, M, Nc, dtype=torch.bfloat16, device="cuda")
+    L.call("ffmoe_gemm_wgrad", a[lo:hi].contiguous().data_ptr(), b[lo:hi].contiguous().data_ptr(),
+           one_off.data_ptr(), 1, M, Nc, c1.data_ptr(), L.stream_ptr())
+    torch.cuda.synchronize()
+    assert torch.equal(c[heavy], c1[0])
+
+
 # --- the whole layer against the oracle -----------------------------------------
 
 def _run_layer(x, gate, wu, wd, k, go, **kw):
