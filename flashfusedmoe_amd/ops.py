@@ -218,6 +218,11 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
            aux_coeff, z_coeff, N, D, E, k, gating, int(capacity_mode), int(aux_through_weights),
            L.ptr(aux_idx), L.ptr(aux_counts), int(pre_softmax), float(scoring), L.ptr(wgo),
            L.ptr(gl), None, st)
+    # the down-projection weight gradient first, while the `wgo` rows the
+    # routing backward just wrote are cache-resident (measured 0.5% faster per
+    # C2 step than after the dX GEMMs)
+    dwd = torch.empty(E, D, H, dtype=_BF16, device=dev)
+    L.call("ffmoe_gemm_wgrad", L.ptr(wgo), L.ptr(act), L.ptr(offsets), E, D, H, L.ptr(dwd), st)
     gup = torch.empty(T, H2, dtype=_BF16, device=dev)
     tr = L.gemm_tile_rows(T, E)
     ws = L.ptr(L.gemm_workspace(dev, st))
@@ -240,8 +245,6 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
         addend = torch.matmul(gl, gate)
         L.call("ffmoe_combine", L.ptr(ghb), L.ptr(row_of), None, L.ptr(addend), N, D, k, L.ptr(dx),
                st)
-    dwd = torch.empty(E, D, H, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_wgrad", L.ptr(wgo), L.ptr(act), L.ptr(offsets), E, D, H, L.ptr(dwd), st)
     if fused_gate:
         dgate = torch.empty(E, D, dtype=_BF16, device=dev)
         part = torch.empty(int(L.load().ffmoe_gate_grad_workspace_bytes(N, D, E)), dtype=torch.uint8,
