@@ -1,6 +1,6 @@
 """Benchmark of the fused MoE layer on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--traffic]
 
 Workload (configuration C2, the reference README's Quick Start layer):
 fused_moe forward + backward, N = 8192 tokens (B=4, T=2048), D = 1024,
@@ -11,11 +11,23 @@ seeded CPU generator: x ~ N(0,1), weights ~ N(0, 1/fan_in), upstream grad
 resident in HBM.  The shared expert of MoELayer is timed separately.
 
 Prints ONE JSON line.  Besides the contract fields it carries:
-  roofline      the dominant kernel's achieved rate vs MI355X peak, from HIP
-                events around repeated launches of that kernel alone;
-  kernels       the same measurement for every hot kernel;
-  cpu_baseline  the reference's unfused PyTorch path (restated in
-                oracle/unfused.py) timed on this host on a bounded sample.
+  roofline       the dominant kernel (the grouped GEMM with the longest
+                 in-step time): algorithmic flops / its average in-step
+                 launch duration (HIP events on the launch stream around
+                 every launch of a run of instrumented steps), vs the bf16
+                 MFMA peak;
+  hbm_rooflines  the same for the bandwidth kernels (scatter = permute,
+                 combine, weighted scatter = route_bwd, gather = dX reduce,
+                 route), in-step and cold (launched alone after a 1 GiB
+                 write that evicts the L2 and the MALL), vs the HBM peak;
+  kernels        in-step duration and rate of every hot kernel;
+  cpu_baseline   the reference's unfused PyTorch path (restated in
+                 oracle/unfused.py) timed on this host on a bounded sample.
+
+``--traffic`` runs each hot kernel twice, after a 256 MiB calibration copy
+and with a 1 GiB flush before every launch, and prints nothing else: the
+driver of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes whose summary
+is profiles/hbm_traffic_c2.md.
 """
 
 import argparse
@@ -35,6 +47,27 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 CFG = dict(N=8192, D=1024, ffn=4096, E=8, k=2, activation="swiglu", gating="softmax",
            aux=0.01, z=1e-3)
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_c2.md")
+
+# entry point -> kernel name(s) in the order a step calls it
+STEP_KERNELS = {
+    "ffmoe_route_fwd_ex": ["route_fwd"],
+    "ffmoe_route_scan": ["route_scan"],
+    "ffmoe_permute": ["permute"],
+    "ffmoe_gemm_up_glu": ["gemm_up_glu"],
+    "ffmoe_gemm_down": ["gemm_down"],
+    "ffmoe_combine": ["combine"],
+    "ffmoe_route_bwd_ex": ["route_bwd"],
+    "ffmoe_gemm_wgrad": ["gemm_wgrad_down", "gemm_wgrad_up"],
+    "ffmoe_gemm_dgrad_glu": ["gemm_dgrad_glu"],
+    "ffmoe_gemm_dgrad": ["gemm_dgrad"],
+    "ffmoe_dx_reduce": ["dx_reduce"],
+    "ffmoe_gate_grad": ["gate_grad"],
+}
+# what each bandwidth kernel is in the reference's vocabulary
+HBM_ROLES = {"permute": "scatter", "combine": "combine", "route_bwd": "weighted scatter",
+             "dx_reduce": "gather", "route_fwd": "route"}
+
 
 def make_inputs(N, D, ffn, E, seed=0):
     g = torch.Generator().manual_seed(seed)
@@ -46,26 +79,38 @@ def make_inputs(N, D, ffn, E, seed=0):
     return x, gate, wu, wd, go
 
 
-def time_events(fn, reps):
-    """Average ms of fn() over reps launches, HIP events on torch's current
-    stream (every ffmoe kernel is launched on that stream)."""
-    fn()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
-        fn()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / reps
-
-
-TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "gemm_hbm_traffic_c2.md")
+def algorithmic_work(c, rows):
+    """Algorithmic flops (GEMMs) or bytes (bandwidth kernels) of one launch
+    at configuration c with `rows` routed rows (N*k at C2: nothing dropped).
+    Padding is never counted."""
+    N, D, E, k = c["N"], c["D"], c["E"], c["k"]
+    H = c["ffn"] // 2
+    T = N * k
+    b = 2  # bytes per bf16
+    up_f = 2.0 * rows * D * 2 * H
+    dn_f = 2.0 * rows * H * D
+    return {
+        "gemm_up_glu": (up_f, "flop"), "gemm_down": (dn_f, "flop"),
+        "gemm_dgrad_glu": (dn_f, "flop"), "gemm_dgrad": (up_f, "flop"),
+        "gemm_wgrad_down": (dn_f, "flop"), "gemm_wgrad_up": (up_f, "flop"),
+        # x, gate read once; idx (8) + w (4) per entry and the bf16 logits written
+        "route_fwd": (N * D * b + E * D * b + T * 12 + N * E * b, "byte"),
+        "route_scan": (None, "byte"),
+        # scatter: token rows read once, routed rows written, idx / row_of
+        "permute": (N * D * b + rows * D * b + T * 12, "byte"),
+        # combine: routed rows read, token rows written, row_of + weight per entry
+        "combine": (rows * D * b + N * D * b + T * 12, "byte"),
+        # weighted scatter + routing-weight grad: go read, down rows read for
+        # the dots, wgo rows written, logits read and grad_logits written
+        "route_bwd": (N * D * b + 2 * rows * D * b + 2 * N * E * b + T * 16, "byte"),
+        # dX gather: ghb rows read, dx written, gl and gate for the gate term
+        "dx_reduce": (rows * D * b + N * D * b + N * E * b + E * D * b + T * 4, "byte"),
+        "gate_grad": (N * D * b + N * E * b + E * D * b, "byte"),
+    }
 
 
 def measured_traffic():
-    """HBM bytes per launch of each grouped GEMM at C2, from the committed
+    """HBM bytes per launch of each hot kernel at C2, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of
     known size); {} when the summary is absent."""
     out = {}
@@ -79,9 +124,64 @@ def measured_traffic():
     return out
 
 
-def kernel_rates(c, x, gate, wu, wd, go, reps=20):
-    """Times each hot kernel alone (launched through the C ABI) and returns
-    {name: {ms, rate, unit, frac, work}} with algorithmic work per launch."""
+class StepRecorder:
+    """Records a HIP event pair around every libffmoe launch (on torch's
+    current stream, where every ffmoe kernel is enqueued) and averages the
+    durations per kernel name."""
+
+    def __init__(self):
+        self.pairs = []   # (kernel name, start event, end event)
+        self.seen = {}
+        self.open = None
+
+    def new_step(self):
+        self.seen = {}
+
+    def __call__(self, name, phase):
+        names = STEP_KERNELS.get(name)
+        if names is None:
+            return
+        if phase == 0:
+            i = self.seen.get(name, 0)
+            self.seen[name] = i + 1
+            label = names[min(i, len(names) - 1)]
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self.open = (label, ev)
+        else:
+            label, ev0 = self.open
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev1.record()
+            self.pairs.append((label, ev0, ev1))
+            self.open = None
+
+    def averages_ms(self):
+        torch.cuda.synchronize()
+        acc = {}
+        for label, e0, e1 in self.pairs:
+            acc.setdefault(label, []).append(e0.elapsed_time(e1))
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def instrumented_steps(step, n):
+    """Runs n steps with every launch bracketed by HIP events; returns the
+    average in-step duration (ms) of each kernel."""
+    from flashfusedmoe_amd import _lib as L
+    rec = StepRecorder()
+    L.call_hook = rec
+    try:
+        for _ in range(n):
+            rec.new_step()
+            step()
+    finally:
+        L.call_hook = None
+    return rec.averages_ms()
+
+
+def kernel_launches(c, x, gate, wu, wd, go):
+    """Standalone launches of every hot kernel of the C2 step through the C
+    ABI, on inputs from one real forward: {name: fn}, plus the routed row
+    count."""
     from flashfusedmoe_amd import _lib as L
     from flashfusedmoe_amd import ops
     N, D, E, k = c["N"], c["D"], c["E"], c["k"]
@@ -97,99 +197,150 @@ def kernel_rates(c, x, gate, wu, wd, go, reps=20):
     st = L.stream_ptr()
     P = L.ptr
     dev = x.device
-    wgo = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
-    gl = torch.empty(N, E, dtype=torch.bfloat16, device=dev)
-    gup = torch.empty(T, 2 * H, dtype=torch.bfloat16, device=dev)
-    ghb = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
-    dwd = torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
-    dwu = torch.empty(E, 2 * H, D, dtype=torch.bfloat16, device=dev)
-    dx = torch.empty(N, D, dtype=torch.bfloat16, device=dev)
+    bf = torch.bfloat16
+    wgo = torch.empty(T, D, dtype=bf, device=dev)
+    gl = torch.empty(N, E, dtype=bf, device=dev)
+    gup = torch.empty(T, 2 * H, dtype=bf, device=dev)
+    ghb = torch.empty(T, D, dtype=bf, device=dev)
+    dwd = torch.empty(E, D, H, dtype=bf, device=dev)
+    dwu = torch.empty(E, 2 * H, D, dtype=bf, device=dev)
+    dx = torch.empty(N, D, dtype=bf, device=dev)
     gpart = torch.empty(int(L.load().ffmoe_gate_grad_workspace_bytes(N, D, E)), dtype=torch.uint8,
                         device=dev)
-    dgate = torch.empty(E, D, dtype=torch.bfloat16, device=dev)
+    dgate = torch.empty(E, D, dtype=bf, device=dev)
     xs2 = torch.empty_like(xs)
     row2 = torch.empty_like(row_of)
     tw3 = tw.clone()
     gz = torch.ones((), device=dev)
-    up_f = 2.0 * rows * D * 2 * H
-    dn_f = 2.0 * rows * H * D
-    b = 2  # bytes per bf16
     tr = L.gemm_tile_rows(T, E)
     gws = P(L.gemm_workspace(xs.device, st))
-    launches = {
-        "gemm_up_glu": (lambda: L.call("ffmoe_gemm_up_glu", P(xs), P(wu), P(off), P(til), tr, E, T, D,
-                                       H, 0, P(up), P(act), gws, st), up_f, "flop"),
-        "gemm_down": (lambda: L.call("ffmoe_gemm_down", P(act), P(wd), P(off), P(til), tr, E, T, H, D,
-                                     P(down), gws, st), dn_f, "flop"),
-        "gemm_dgrad_glu": (lambda: L.call("ffmoe_gemm_dgrad_glu", P(wgo), P(wd), P(up), P(off), P(til),
-                                          tr, E, T, D, H, 0, P(gup), gws, st), dn_f, "flop"),
-        "gemm_dgrad": (lambda: L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), tr, E, T, H,
-                                      D, P(ghb), gws, st), up_f, "flop"),
-        "gemm_wgrad_down": (lambda: L.call("ffmoe_gemm_wgrad", P(wgo), P(act), P(off), E, D, H, P(dwd),
-                                           st), dn_f, "flop"),
-        "gemm_wgrad_up": (lambda: L.call("ffmoe_gemm_wgrad", P(gup), P(xs), P(off), E, 2 * H, D, P(dwu),
-                                         st), up_f, "flop"),
-        # bandwidth kernels: algorithmic bytes (read token rows once, write k rows)
-        "route_fwd": (lambda: L.call("ffmoe_route_fwd", P(x), P(gate), None, None, N, D, E, k, 0, 0,
-                                     P(logits), P(idx), P(tw3), P(lse), P(ws), st),
-                      N * D * b + E * D * b + N * k * 12 + N * E * b, "byte"),
-        "permute": (lambda: L.call("ffmoe_permute", P(x), P(idx), P(tw3), P(off), P(counts), N, D, E, k,
-                                   mt, 0, P(ws), P(xs2), P(row2), st),
-                    N * D * b + rows * D * b + N * k * 12, "byte"),
-        "combine": (lambda: L.call("ffmoe_combine", P(down), P(row_of), P(tw), None, N, D, k, P(out),
-                                   st), rows * D * b + N * D * b + N * k * 8, "byte"),
-        "route_bwd": (lambda: L.call("ffmoe_route_bwd", P(go), P(down), P(row_of), P(idx), P(tw),
-                                     P(logits), P(lse), P(counts), None, P(gz), c["aux"], c["z"], N, D,
-                                     E, k, 0, 0, P(wgo), P(gl), None, st),
-                      N * D * b + 2 * rows * D * b + N * E * 2 * b + N * k * 16, "byte"),
-        "dx_reduce": (lambda: L.call("ffmoe_dx_reduce", P(ghb), P(row_of), P(gl), P(gate), N, D, E, k,
-                                     P(dx), st),
-                      rows * D * b + N * D * b + N * E * b + E * D * b + N * k * 4, "byte"),
-        "gate_grad": (lambda: L.call("ffmoe_gate_grad", P(gl), P(x), N, D, E, P(gpart), P(dgate), st),
-                      N * D * b + N * E * b + E * D * b, "byte"),
+    # realistic operands for the backward GEMMs: one routing backward first
+    L.call("ffmoe_route_bwd", P(go), P(down), P(row_of), P(idx), P(tw), P(logits), P(lse), P(counts),
+           None, P(gz), c["aux"], c["z"], N, D, E, k, 0, 0, P(wgo), P(gl), None, st)
+    L.call("ffmoe_gemm_dgrad_glu", P(wgo), P(wd), P(up), P(off), P(til), tr, E, T, D, H, 0, P(gup),
+           gws, st)
+    L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), tr, E, T, H, D, P(ghb), gws, st)
+    fns = {
+        "gemm_up_glu": lambda: L.call("ffmoe_gemm_up_glu", P(xs), P(wu), P(off), P(til), tr, E, T, D,
+                                      H, 0, P(up), P(act), gws, st),
+        "gemm_down": lambda: L.call("ffmoe_gemm_down", P(act), P(wd), P(off), P(til), tr, E, T, H, D,
+                                    P(down), gws, st),
+        "gemm_dgrad_glu": lambda: L.call("ffmoe_gemm_dgrad_glu", P(wgo), P(wd), P(up), P(off), P(til),
+                                         tr, E, T, D, H, 0, P(gup), gws, st),
+        "gemm_dgrad": lambda: L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), tr, E, T, H,
+                                     D, P(ghb), gws, st),
+        "gemm_wgrad_down": lambda: L.call("ffmoe_gemm_wgrad", P(wgo), P(act), P(off), E, D, H, P(dwd),
+                                          st),
+        "gemm_wgrad_up": lambda: L.call("ffmoe_gemm_wgrad", P(gup), P(xs), P(off), E, 2 * H, D, P(dwu),
+                                        st),
+        "route_fwd": lambda: L.call("ffmoe_route_fwd", P(x), P(gate), None, None, N, D, E, k, 0, 0,
+                                    P(logits), P(idx), P(tw3), P(lse), P(ws), st),
+        "permute": lambda: L.call("ffmoe_permute", P(x), P(idx), P(tw3), P(off), P(counts), N, D, E, k,
+                                  mt, 0, P(ws), P(xs2), P(row2), st),
+        "combine": lambda: L.call("ffmoe_combine", P(down), P(row_of), P(tw), None, N, D, k, P(out),
+                                  st),
+        "route_bwd": lambda: L.call("ffmoe_route_bwd", P(go), P(down), P(row_of), P(idx), P(tw),
+                                    P(logits), P(lse), P(counts), None, P(gz), c["aux"], c["z"], N, D,
+                                    E, k, 0, 0, P(wgo), P(gl), None, st),
+        "dx_reduce": lambda: L.call("ffmoe_dx_reduce", P(ghb), P(row_of), P(gl), P(gate), N, D, E, k,
+                                    P(dx), st),
+        "gate_grad": lambda: L.call("ffmoe_gate_grad", P(gl), P(x), N, D, E, P(gpart), P(dgate), st),
     }
-    res = {}
-    for name, (fn, work, kind) in launches.items():
-        ms = time_events(fn, reps)
-        if kind == "flop":
-            rate = work / (ms * 1e-3) / 1e12
-            res[name] = dict(ms=ms, rate=rate, unit="TFLOP/s", frac=rate / PEAK_BF16_TFLOPS,
-                             work=work, bound="mfma")
-        else:
-            rate = work / (ms * 1e-3) / 1e9
-            res[name] = dict(ms=ms, rate=rate, unit="GB/s", frac=rate / PEAK_HBM_GBS, work=work,
-                             bound="hbm")
-    return res
+    keep = (logits, idx, tw, lse, counts, off, til, ws, out, row_of, xs, up, act, down, wgo, gl, gup,
+            ghb, dwd, dwu, dx, gpart, dgate, xs2, row2, tw3, gz)
+    return fns, rows, keep
 
 
-def cpu_baseline(c, sample_tokens):
+def cold_launch_ms(fn, flush, reps):
+    """Average duration (ms) of fn() launched alone after a write of `flush`
+    (1 GiB: evicts the 4 MiB L2s and the 256 MiB MALL), HIP events on the
+    launch stream around the kernel only."""
+    fn()
+    torch.cuda.synchronize()
+    pairs = []
+    for _ in range(reps):
+        flush.zero_()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        pairs.append((e0, e1))
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in pairs) / reps
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(c, sample_tokens, runs=7):
     """The reference's unfused CPU path (oracle/unfused.py restates
     tests/conftest.py:58-137) forward + backward in fp32 on a bounded sample
-    of the workload: sample_tokens tokens, the full expert weights."""
+    of the workload: sample_tokens tokens, the full expert weights; median
+    of `runs` after one warm-up.  Threads: every core this process may use
+    (os.cpu_count(), capped by OMP_NUM_THREADS where the host sets the
+    process's CPU share)."""
     from oracle.unfused import unfused_moe
-    threads = torch.get_num_threads()
-    x, gate, wu, wd, go = make_inputs(sample_tokens, c["D"], c["ffn"], c["E"], seed=1)
-    leaves = [t.clone().requires_grad_(True) for t in (x, gate, wu, wd)]
+    ncpu = os.cpu_count() or 1
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(ncpu, cap) if cap > 0 else ncpu
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        x, gate, wu, wd, go = make_inputs(sample_tokens, c["D"], c["ffn"], c["E"], seed=1)
+        leaves = [t.clone().requires_grad_(True) for t in (x, gate, wu, wd)]
 
-    def step():
-        for t in leaves:
-            t.grad = None
-        out, _, _, losses = unfused_moe(*leaves, c["k"], activation=c["activation"],
-                                        aux_loss_coeff=c["aux"], z_loss_coeff=c["z"])
-        torch.autograd.backward([out, losses["aux_loss"], losses["z_loss"]],
-                                [go, torch.ones(()), torch.ones(())])
+        def step():
+            for t in leaves:
+                t.grad = None
+            out, _, _, losses = unfused_moe(*leaves, c["k"], activation=c["activation"],
+                                            aux_loss_coeff=c["aux"], z_loss_coeff=c["z"])
+            torch.autograd.backward([out, losses["aux_loss"], losses["z_loss"]],
+                                    [go, torch.ones(()), torch.ones(())])
 
-    step()
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
         step()
-        times.append(time.perf_counter() - t0)
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
+        used = torch.get_num_threads()
+    finally:
+        torch.set_num_threads(prev)
     times.sort()
-    med = times[1]
-    return dict(value=sample_tokens / med, unit="tokens/s", cores=threads, kind="port",
+    med = times[len(times) // 2]
+    return dict(value=sample_tokens / med, unit="tokens/s", cores=used, cpu_count=ncpu,
+                torch_threads=used, cpu_model=cpu_model(), kind="port",
                 sample=f"{sample_tokens} tokens of the C2 layer (D1024 ffn4096 E8 k2 swiglu, aux+z), "
-                       f"fp32 fwd+bwd, median of 3 after 1 warm-up ({med:.2f} s/run)")
+                       f"fp32 fwd+bwd, median of {runs} after 1 warm-up ({med:.2f} s/run, "
+                       f"{sum(times):.1f} s timed)")
+
+
+def traffic_mode(c, x, gate, wu, wd, go):
+    """Each hot kernel twice, after a 256 MiB calibration copy, with a 1 GiB
+    flush before every launch (the rocprofv3 --pmc driver)."""
+    fns, _, keep = kernel_launches(c, x, gate, wu, wd, go)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=x.device)
+    src = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=x.device).uniform_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written
+    torch.cuda.synchronize()
+    del src, dst
+    for name, fn in fns.items():
+        for _ in range(2):
+            flush.zero_()
+            fn()
+        torch.cuda.synchronize()
+        print(f"traffic: {name} launched twice", flush=True)
+    del keep
+    print("traffic done", flush=True)
 
 
 def main():
@@ -201,6 +352,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--no-kernels", action="store_true", help="skip per-kernel timing")
     ap.add_argument("--no-layer", action="store_true", help="skip the MoELayer (shared expert) timing")
+    ap.add_argument("--instr-steps", type=int, default=10, help="instrumented steps for in-step kernel times")
+    ap.add_argument("--traffic", action="store_true", help="rocprofv3 --pmc driver mode")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -213,6 +366,9 @@ def main():
     c = CFG
     dev = torch.device("cuda:0")
     x, gate, wu, wd, go = (t.to(torch.bfloat16).to(dev) for t in make_inputs(c["N"], c["D"], c["ffn"], c["E"]))
+    if args.traffic:
+        traffic_mode(c, x, gate, wu, wd, go)
+        return
     params = [t.requires_grad_(True) for t in (x, gate, wu, wd)]
     one = torch.ones((), device=dev)
 
@@ -241,34 +397,75 @@ def main():
     expert_flop = 3 * (2.0 * T * c["D"] * 2 * H + 2.0 * T * H * c["D"])
     step_mfma_frac = expert_flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS
 
+    kernels, roofline, hbm = {}, None, {}
+    if not args.no_kernels:
+        in_step = instrumented_steps(step, args.instr_steps)
+        xd, gd, ud, dd = (p.detach() for p in params)
+        fns, rows, keep = kernel_launches(c, xd, gd, ud, dd, go)
+        work = algorithmic_work(c, rows)
+        flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        traffic = measured_traffic()
+        for name, ms_in in sorted(in_step.items()):
+            w, kind = work.get(name, (None, "byte"))
+            ent = {"in_step_ms": round(ms_in, 5)}
+            if w is not None:
+                if kind == "flop":
+                    rate = w / (ms_in * 1e-3) / 1e12
+                    ent.update(rate=round(rate, 2), unit="TFLOP/s", frac=round(rate / PEAK_BF16_TFLOPS, 4))
+                else:
+                    rate = w / (ms_in * 1e-3) / 1e9
+                    ent.update(rate=round(rate, 1), unit="GB/s", frac=round(rate / PEAK_HBM_GBS, 4))
+            kernels[name] = ent
+        gemms = [n for n in kernels if n.startswith("gemm_")]
+        if gemms:
+            dom = max(gemms, key=lambda n: kernels[n]["in_step_ms"])
+            d = kernels[dom]
+            roofline = dict(kernel=dom, bound="mfma", achieved=d["rate"], peak=PEAK_BF16_TFLOPS,
+                            unit="TFLOP/s", frac=d["frac"], traffic=traffic.get(dom),
+                            algorithmic_flop=work[dom][0], avg_launch_ms=d["in_step_ms"],
+                            timing="in-step: HIP events around every launch of "
+                                   f"{args.instr_steps} instrumented fwd+bwd steps")
+        for name, role in HBM_ROLES.items():
+            if name not in kernels:
+                continue
+            w = work[name][0]
+            cold = cold_launch_ms(fns[name], flush, 20)
+            kernels[name]["cold_ms"] = round(cold, 5)
+            a_in = w / (kernels[name]["in_step_ms"] * 1e-3) / 1e9
+            a_cold = w / (cold * 1e-3) / 1e9
+            hbm[name] = dict(role=role, bound="hbm", achieved=round(a_in, 1), peak=PEAK_HBM_GBS,
+                             unit="GB/s", frac=round(a_in / PEAK_HBM_GBS, 4),
+                             cold_achieved=round(a_cold, 1), cold_frac=round(a_cold / PEAK_HBM_GBS, 4),
+                             traffic=traffic.get(name), algorithmic_bytes=int(w))
+        del keep, flush
+
     # MoELayer with the shared expert (config C2 as the reference's README quotes it)
-    torch.manual_seed(0)
-    layer = MoELayer(c["D"], c["ffn"], c["E"], top_k=c["k"], num_shared_experts=1,
-                     aux_loss_coeff=c["aux"], z_loss_coeff=c["z"]).to(dev, torch.bfloat16)
-    xl = x.detach().clone().requires_grad_(True)
+    layer_ms = None
+    if not args.no_layer:
+        torch.manual_seed(0)
+        layer = MoELayer(c["D"], c["ffn"], c["E"], top_k=c["k"], num_shared_experts=1,
+                         aux_loss_coeff=c["aux"], z_loss_coeff=c["z"]).to(dev, torch.bfloat16)
+        xl = x.detach().clone().requires_grad_(True)
 
-    def layer_step():
-        layer.zero_grad(set_to_none=True)
-        xl.grad = None
-        out, losses = layer(xl)
-        torch.autograd.backward([out, losses["z_loss"]], [go, one])
+        def layer_step():
+            layer.zero_grad(set_to_none=True)
+            xl.grad = None
+            out, losses = layer(xl)
+            torch.autograd.backward([out, losses["z_loss"]], [go, one])
 
-    layer_ms = None if args.no_layer else time_events(layer_step, max(5, args.steps // 2))
+        for _ in range(3):
+            layer_step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = max(5, args.steps // 2)
+        e0.record()
+        for _ in range(reps):
+            layer_step()
+        e1.record()
+        torch.cuda.synchronize()
+        layer_ms = e0.elapsed_time(e1) / reps
 
-    kernels = {} if args.no_kernels else kernel_rates(
-        c, *(p.detach() for p in params), go)
-    gemms = {n: v for n, v in kernels.items() if v["bound"] == "mfma"}
-    dom_name = max(gemms, key=lambda n: gemms[n]["ms"]) if gemms else None
-    roofline = None
-    if dom_name:
-        d = kernels[dom_name]
-        roofline = dict(kernel=dom_name, bound="mfma", achieved=round(d["rate"], 2),
-                        peak=PEAK_BF16_TFLOPS, unit="TFLOP/s", frac=round(d["frac"], 4),
-                        traffic=measured_traffic().get(dom_name))
-
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(c, args.cpu_tokens)
+    cpu = None if args.no_cpu else cpu_baseline(c, args.cpu_tokens)
 
     line = {
         "metric": "fused_moe fwd+bwd tokens/s (D1024 E8 k2 bf16); % bf16 MFMA peak; HBM GB/s",
@@ -290,8 +487,8 @@ def main():
         "moelayer_shared_expert": None if layer_ms is None else {
             "ms_per_step": round(layer_ms, 4), "tokens_per_s": round(c["N"] / (layer_ms * 1e-3), 1)},
         "roofline": roofline,
-        "kernels": {n: {"ms": round(v["ms"], 5), "rate": round(v["rate"], 2), "unit": v["unit"],
-                        "frac": round(v["frac"], 4)} for n, v in kernels.items()},
+        "hbm_rooflines": hbm,
+        "kernels": kernels,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }

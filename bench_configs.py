@@ -1,7 +1,6 @@
 """Step timing of fused_moe at the reference benchmark's other configurations.
 
-    python -m flashfusedmoe_amd.bench_configs [--config c3|c4|c5|all] [--steps K] [--warmup W]
-    python flashfusedmoe_amd/bench_configs.py ...      # same, from any directory
+    python bench_configs.py [--config c3|c4|c5|all] [--steps K] [--warmup W]
 
 bench.py measures the headline configuration (C2); this runs the others on
 one GPU, with synthetic inputs of the stated shapes and distributions, and
@@ -30,7 +29,7 @@ import time
 
 import torch
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 

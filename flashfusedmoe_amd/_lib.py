@@ -42,6 +42,7 @@ SIGNATURES = {
     "ffmoe_gemm_tile_rows": (_I, [_L, _I]),
     "ffmoe_set_lds_transpose": (_I, [_I]),
     "ffmoe_gemm_workspace_bytes": (_L, []),
+    "ffmoe_gemm_check": (_I, [_P, _P]),
     "ffmoe_gemm_up_glu": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P, _P]),
     "ffmoe_gemm_down": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P]),
     "ffmoe_gemm_dgrad_glu": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
@@ -58,6 +59,7 @@ SIGNATURES = {
     "ffmoe_glu_fwd": (_I, [_P, _L, _I, _I, _P, _P]),
     "ffmoe_glu_bwd": (_I, [_P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_scatter_rows": (_I, [_P, _P, _P, _L, _I, _I, _L, _P, _P]),
+    "ffmoe_routing_scatter_padded": (_I, [_P, _P, _P, _P, _L, _I, _I, _L, _I, _L, _P, _P, _P]),
 }
 
 _lib = None
@@ -100,11 +102,22 @@ def stream_ptr(device=None):
     return torch.cuda.current_stream(device).cuda_stream
 
 
+# Optional observer of every entry-point call: hook(name, phase) with phase 0
+# right before and 1 right after the call (a profiler records HIP events on
+# the launch stream there).  None in normal use.
+call_hook = None
+
+
 def call(name, *args):
     """Calls an entry point and raises FFMoEError with the library's message
     when it returns nonzero."""
     lib = load()
+    hook = call_hook
+    if hook is not None:
+        hook(name, 0)
     rc = getattr(lib, name)(*args)
+    if hook is not None:
+        hook(name, 1)
     if rc != 0:
         msg = lib.ffmoe_last_error().decode(errors="replace")
         raise FFMoEError(f"{name} failed: {msg}")
@@ -134,6 +147,16 @@ def gemm_workspace(device, stream):
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _GEMM_WS[key] = ws
     return ws
+
+
+def check_gemm_workspaces():
+    """Raises FFMoEError if a grouped GEMM on any cached workspace reported a
+    timed-out stream-K wait (its output was wrong); the workspace is cleared
+    first, so later calls are sound.  Synchronises each workspace's stream."""
+    import torch
+    for (dev, stream), ws in list(_GEMM_WS.items()):
+        with torch.cuda.device(dev):
+            call("ffmoe_gemm_check", ws.data_ptr(), stream)
 
 
 def route_workspace_bytes(N, E, k):

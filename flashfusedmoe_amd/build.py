@@ -15,7 +15,15 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libffmoe.so")
-SOURCES = ("status.hip", "route.hip", "combine.hip", "gemm.hip")
+# (source, object, extra flags): route.hip is compiled once per expert-count
+# tier of its routing kernel (FFMOE_ROUTE_PART), so the units build in parallel
+UNITS = (
+    ("status.hip", "status.o", ()),
+    ("route.hip", "route.o", ("-DFFMOE_ROUTE_PART=0",)),
+    *((("route.hip", f"route_et{et}.o", (f"-DFFMOE_ROUTE_PART={et}",)) for et in (1, 2, 4, 8, 16))),
+    ("combine.hip", "combine.o", ()),
+    ("gemm.hip", "gemm.o", ()),
+)
 ARCH = os.environ.get("FFMOE_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -28,8 +36,10 @@ FLAGS = [
 ]
 
 
-def _compile(src, obj):
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(unit, objdir):
+    src, obj, extra = unit
+    obj = os.path.join(objdir, obj)
+    cmd = [HIPCC, *FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
@@ -40,9 +50,9 @@ def build(verbose=True):
     """Compiles every source and links libffmoe.so next to this file."""
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = [os.path.join(objdir, s.replace(".hip", ".o")) for s in SOURCES]
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
-        list(ex.map(_compile, SOURCES, objs))
+    jobs = max(1, min(len(UNITS), int(os.environ.get("MAX_JOBS", "8"))))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda u: _compile(u, objdir), UNITS))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -621,9 +621,55 @@ static inline unsigned grid_for(int64_t units) {
   return static_cast<unsigned>(b);
 }
 
+// The reference's padded routing scatter (moe_ops.py:43-106): sorted
+// position p names entry j = sorted_order[p] of expert e = flat_ids[j] with
+// rank p - starts[e]; an entry of rank < mt gets e2b[j] = e*mt + rank and
+// its token's row x[j / k] is copied to out[e2b[j]].  Entries of rank >= mt
+// are skipped (their e2b keeps the caller's zero).  Indices outside their
+// tensors are skipped too, so malformed routing cannot address memory
+// outside the buffers.  One 16-byte vector per thread, grid-stride.
+__global__ __launch_bounds__(256) void routing_scatter_kernel(
+    const int64_t* __restrict__ sorted_order, const int64_t* __restrict__ flat_ids,
+    const int64_t* __restrict__ starts, const bf16_t* __restrict__ x, int64_t n_sorted, int64_t NK,
+    int D, int E, int64_t mt, int k, bf16_t* __restrict__ out, int64_t* __restrict__ e2b) {
+  const int nvec = D / 8;
+  const int64_t total = n_sorted * nvec;
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
+       u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t p = u / nvec;
+    const int v = static_cast<int>(u % nvec);
+    const int64_t j = sorted_order[p];
+    if (j < 0 || j >= NK) continue;
+    const int64_t e = flat_ids[j];
+    if (e < 0 || e >= E) continue;
+    const int64_t rank = p - starts[e];
+    if (rank < 0 || rank >= mt) continue;
+    const int64_t pos = e * mt + rank;
+    if (v == 0) e2b[j] = pos;
+    reinterpret_cast<uint4*>(out + pos * D)[v] = reinterpret_cast<const uint4*>(x + (j / k) * D)[v];
+  }
+}
+
 }  // namespace ffmoe
 
 using namespace ffmoe;
+
+extern "C" int ffmoe_routing_scatter_padded(const int64_t* sorted_order, const int64_t* flat_ids,
+                                            const int64_t* starts, const void* x, int64_t N, int D,
+                                            int E, int64_t mt, int k, int64_t n_sorted, void* out,
+                                            int64_t* e2b, void* stream) {
+  if (N < 0 || D <= 0 || D % 8 != 0)
+    return set_error("ffmoe_routing_scatter_padded: D must be a positive multiple of 8");
+  if (E < 1 || k < 1 || mt < 0 || n_sorted < 0 || n_sorted > N * k)
+    return set_error("ffmoe_routing_scatter_padded: bad E, k, max_tokens or num_sorted");
+  if (n_sorted == 0) return clear_error();
+  hipLaunchKernelGGL(routing_scatter_kernel, dim3(grid_for(n_sorted * (D / 8))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), sorted_order, flat_ids, starts,
+                     static_cast<const bf16_t*>(x), n_sorted, N * k, D, E, mt, k,
+                     static_cast<bf16_t*>(out), e2b);
+  if (check_launch("routing_scatter_kernel")) return 1;
+  return clear_error();
+}
 
 extern "C" int ffmoe_combine(const void* rows, const int32_t* row_of, const float* topk_w,
                              const void* addend, int64_t N, int D, int k, void* out, void* stream) {

@@ -869,13 +869,17 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
       while ((src = __hip_atomic_load(p.flags + gridDim.x + key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0 &&
              ++polls < kSpinLimit)
         __builtin_amdgcn_s_sleep(8);
-      __hip_atomic_store(p.flags + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.flags + gridDim.x + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (polls >= kSpinLimit) {  // never expected: report through the error word
+      if (src != 0) {
+        __hip_atomic_store(p.flags + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.flags + gridDim.x + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        // Never expected.  The tile is finished without the partner's
+        // partial and the error word is set; both flag words are left as
+        // they are (the partner may still publish), so the workspace stays
+        // unusable until ffmoe_gemm_check() reports the error and clears it.
         __hip_atomic_store(p.flags + 2 * gridDim.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        src = slot + 1;  // add nothing meaningful rather than read a wild slot
       }
-      *s_word = src - 1;
+      *s_word = src - 1;  // -1: no partial to add
     }
     __syncthreads();  // the partial is read below with device-scope loads
     partner = *s_word;
@@ -892,7 +896,8 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   const int lr = lane & 31;
   const int lq = (lane >> 5) * 4;
   const __amdgpu_buffer_rsrc_t rpart =
-      make_rsrc(p.part + static_cast<int64_t>(partner) * NF * kThreads * 4, NF * kThreads * 16);
+      make_rsrc(p.part + static_cast<int64_t>(partner < 0 ? 0 : partner) * NF * kThreads * 4,
+                NF * kThreads * 16);
   auto stage = [&](auto add) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
@@ -927,7 +932,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   constexpr int PIT = (EPI == EPI_GLU_BWD) ? glu_bwd_items<BM, BN>() : 1;
   uint4 pre_g[PIT], pre_u[PIT];
   if constexpr (EPI == EPI_GLU_BWD) glu_bwd_prefetch<BM, BN>(p, row_begin, row_end, n0, pre_g, pre_u);
-  if (role == ROLE_CUT) stage(std::true_type{});
+  if (role == ROLE_CUT && partner >= 0) stage(std::true_type{});
   else stage(std::false_type{});
   __syncthreads();
   if constexpr (EPI == EPI_GLU_BWD)
@@ -1187,6 +1192,27 @@ extern "C" int ffmoe_gemm_tile_rows(int64_t max_rows, int E) {
 extern "C" int64_t ffmoe_gemm_workspace_bytes(void) {
   const int G = sk_blocks();
   return G > 0 ? kSkFlagBytes + 2 * static_cast<int64_t>(G) * kSkSlotBytes : -1;
+}
+
+extern "C" int ffmoe_gemm_check(void* sk_workspace, void* stream) {
+  if (sk_workspace == nullptr) return clear_error();
+  const int G = sk_blocks();
+  if (G <= 0) return set_error("ffmoe_gemm_check: cannot query the CU count");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int err = 0;
+  const char* base = static_cast<const char*>(sk_workspace);
+  if (hipMemcpyAsync(&err, base + 2 * static_cast<int64_t>(G) * 4, sizeof(int), hipMemcpyDeviceToHost, st) !=
+          hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return set_error("ffmoe_gemm_check: cannot read the workspace's error word");
+  if (err == 0) return clear_error();
+  // every block of the failed launch has finished (the stream is idle), so
+  // clearing the flag words here cannot race a late publication
+  if (hipMemsetAsync(sk_workspace, 0, kSkFlagBytes, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+    return set_error("ffmoe_gemm_check: cannot clear the workspace");
+  return set_error(
+      "ffmoe_gemm_check: a stream-K partner wait timed out in an earlier grouped GEMM on this workspace; "
+      "that GEMM's output is wrong (the workspace has been cleared)");
 }
 
 extern "C" int ffmoe_set_lds_transpose(int enable) {

@@ -10,6 +10,10 @@
 
 #include "common.h"
 
+#ifndef FFMOE_ROUTE_PART
+#define FFMOE_ROUTE_PART 0
+#endif
+
 namespace ffmoe {
 
 // Tokens per route block: one wave of 16 (one MFMA row tile).  Small blocks
@@ -444,6 +448,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
 // long trip), the chunk sums are scanned across the runs in LDS (log2 G
 // steps), then a second pass writes the bases.  Every sum is a fixed tree or
 // sequence (deterministic).
+#if FFMOE_ROUTE_PART == 0
 constexpr int kScanThreads = 1024;
 constexpr int kScanBatch = 8;
 
@@ -759,6 +764,8 @@ __global__ __launch_bounds__(256) void permute_kernel(
   }
 }
 
+#endif  // FFMOE_ROUTE_PART == 0
+
 template <int ET, int KMAX, bool FL>
 static void launch_route(dim3 grid, size_t shm, hipStream_t st, const bf16_t* x, const bf16_t* gate,
                          const bf16_t* li, const RouteOpts& o, int64_t N, int D, int E, int k,
@@ -782,7 +789,7 @@ static void launch_route_fl(bool fl, dim3 grid, size_t shm, hipStream_t st, cons
 }
 
 template <int ET>
-static void launch_route_k(int k, bool fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
+void launch_route_k(int k, bool fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
                            const bf16_t* gate, const bf16_t* li, const RouteOpts& o, int64_t N,
                            int D, int E, int gating, int need_ssum, bf16_t* lo, int64_t* ti,
                            float* tw, float* lse, int32_t* rl, RouteWs ws) {
@@ -800,7 +807,29 @@ static void launch_route_k(int k, bool fl, dim3 grid, size_t shm, hipStream_t st
 #undef FFMOE_RK
 }
 
+// The route kernel has 8 instantiations per expert-count tier ET; each tier
+// is compiled in a translation unit of its own (FFMOE_ROUTE_PART = ET), in
+// parallel, and part 0 holds everything else.
+#define FFMOE_ROUTE_K_INST(ETV)                                                                     \
+  template void launch_route_k<ETV>(int, bool, dim3, size_t, hipStream_t, const bf16_t*,         \
+                                    const bf16_t*, const bf16_t*, const RouteOpts&, int64_t, int, \
+                                    int, int, int, bf16_t*, int64_t*, float*, float*, int32_t*,    \
+                                    RouteWs)
+#if FFMOE_ROUTE_PART > 0
+FFMOE_ROUTE_K_INST(FFMOE_ROUTE_PART);
+#else
+#define FFMOE_ROUTE_K_EXT(ETV) extern FFMOE_ROUTE_K_INST(ETV)
+FFMOE_ROUTE_K_EXT(1);
+FFMOE_ROUTE_K_EXT(2);
+FFMOE_ROUTE_K_EXT(4);
+FFMOE_ROUTE_K_EXT(8);
+FFMOE_ROUTE_K_EXT(16);
+#undef FFMOE_ROUTE_K_EXT
+#endif
+
 }  // namespace ffmoe
+
+#if FFMOE_ROUTE_PART == 0
 
 using namespace ffmoe;
 
@@ -929,3 +958,5 @@ extern "C" int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk
   if (check_launch("permute_kernel")) return 1;
   return clear_error();
 }
+
+#endif  // FFMOE_ROUTE_PART == 0

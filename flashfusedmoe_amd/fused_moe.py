@@ -147,6 +147,9 @@ class _FusedMoEFunction(torch.autograd.Function):
 
         if not capacity_mode and not allow_dropped:
             actual_max = int(istats_d[L.ISTAT_MAX].item())          # fused_moe.py:400-410
+            # the stream is idle here anyway: surface a failed stream-K wait
+            # of an earlier call's GEMMs before anything else runs
+            L.check_gemm_workspaces()
             if actual_max > mt:
                 raise RuntimeError(_overflow_message(actual_max, mt))
 

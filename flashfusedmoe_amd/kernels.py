@@ -47,19 +47,17 @@ def fused_routing_scatter(sorted_order, flat_expert_ids, expert_starts, hidden_s
     x = _gpu_bf16("hidden_states", hidden_states)
     N, D = x.shape
     dev = x.device
-    ns = sorted_order.numel() if num_sorted is None else num_sorted
-    p = torch.arange(ns, device=dev)
-    j = sorted_order[:ns]
-    e = flat_expert_ids[j]
-    rank = p - expert_starts[e]
-    valid = rank < max_tokens
-    e2b = torch.zeros(N * top_k, dtype=torch.int64, device=dev)
-    e2b[j[valid]] = (e * max_tokens + rank)[valid]
-    dst = torch.full((N * top_k,), -1, dtype=torch.int64, device=dev)
-    dst[j[valid]] = e2b[j[valid]]
+    ns = N * top_k if num_sorted is None else int(num_sorted)
+    so = sorted_order.to(device=dev, dtype=torch.int64).contiguous()
+    fl = flat_expert_ids.to(device=dev, dtype=torch.int64).contiguous()
+    st = expert_starts.to(device=dev, dtype=torch.int64).contiguous()
+    if so.numel() < ns or fl.numel() != N * top_k or st.numel() < E + 1:
+        raise ValueError("fused_routing_scatter: sorted_order, flat_expert_ids or expert_starts "
+                         "is shorter than the problem")
     out = torch.zeros(E * max_tokens, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_scatter_rows", L.ptr(x), L.ptr(dst), None, N * top_k, top_k, D, E * max_tokens,
-           L.ptr(out), L.stream_ptr(dev))
+    e2b = torch.zeros(N * top_k, dtype=torch.int64, device=dev)
+    L.call("ffmoe_routing_scatter_padded", L.ptr(so), L.ptr(fl), L.ptr(st), L.ptr(x), N, D, E,
+           max_tokens, top_k, ns, L.ptr(out), L.ptr(e2b), L.stream_ptr(dev))
     return out, e2b
 
 

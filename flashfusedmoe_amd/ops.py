@@ -7,6 +7,7 @@ Fake (meta) implementations make the ops traceable by torch.compile.
 Only bfloat16 CUDA(ROCm) tensors are accepted; there is no other path.
 """
 
+import os
 from typing import List, Optional
 
 import torch
@@ -15,6 +16,9 @@ from torch import Tensor
 from . import _lib as L
 
 _BF16 = torch.bfloat16
+# FFMOE_CHECK_GEMM=1: check the grouped GEMMs' stream-K workspace after every
+# expert forward / backward (synchronises the stream; a debugging aid)
+_CHECK_GEMM = os.environ.get("FFMOE_CHECK_GEMM", "0") not in ("", "0")
 
 
 def _require(cond, msg):
@@ -160,6 +164,8 @@ def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, t
                              save_activations, st)
     out = torch.empty(N, D, dtype=_BF16, device=dev)
     L.call("ffmoe_combine", L.ptr(down), L.ptr(row_of), L.ptr(tw), None, N, D, k, L.ptr(out), st)
+    if _CHECK_GEMM:
+        L.check_gemm_workspaces()
     tw_out = tw if capacity_mode else topk_w.new_empty(0)
     empty = x.new_empty(0)
     if not save_activations:
@@ -252,6 +258,8 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
         L.call("ffmoe_gate_grad", L.ptr(gl), L.ptr(x), N, D, E, L.ptr(part), L.ptr(dgate), st)
     else:
         dgate = torch.matmul(gl.t().contiguous(), x)
+    if _CHECK_GEMM:
+        L.check_gemm_workspaces()
     return [dx, dgate, dwu, dwd]
 
 

@@ -180,6 +180,17 @@ int ffmoe_gemm_tile_rows(int64_t max_rows, int E);
  * No reference counterpart (the reference's GEMMs are cuBLAS bmm calls). */
 int64_t ffmoe_gemm_workspace_bytes(void);
 
+/* Reports a failed stream-K partner wait of an earlier grouped GEMM on
+ * sk_workspace.  The wait is bounded; it is not expected to time out (the
+ * block it waits for is already running), but if it does the GEMM's output
+ * is wrong and the kernel sets an error word in the workspace.  This call
+ * synchronises `stream`, reads that word and returns 0 if it is clear;
+ * otherwise it zeroes the workspace's flags (so later calls are sound again)
+ * and returns nonzero with the message in ffmoe_last_error().  No reference
+ * counterpart (the reference's GEMMs are cuBLAS bmm calls, which report no
+ * such condition). */
+int ffmoe_gemm_check(void* sk_workspace, void* stream);
+
 /* up = x_sorted · w_up[e]^T and the fused GLU:
  *   up_out [rows, 2H] (pre-activation, may be NULL), act_out [rows, H].
  * Replaces: up bmm (fused_moe.py:435) + `activation_forward`
@@ -308,6 +319,19 @@ int ffmoe_glu_bwd(const void* grad_act, const void* up, int64_t M, int H,
 int ffmoe_scatter_rows(const void* src, const int64_t* dst_row, const float* w,
                        int64_t n_entries, int k, int D, int64_t dst_rows,
                        void* dst, void* stream);
+
+/* The reference's padded-layout routing scatter, for callers of its
+ * kernel-level boundary (`fused_routing_scatter`, moe_ops.py:43-149): for
+ * sorted position p < n_sorted, j = sorted_order[p], e = flat_ids[j],
+ * rank = p - starts[e]; if rank < mt then e2b[j] = e*mt + rank and
+ * out[e2b[j]] = x[j / k].  sorted_order [n_sorted], flat_ids [N*k],
+ * starts [E+1] int64 (the reference's argsort / bincount / cumsum results);
+ * x [N,D] bf16; out [E*mt, D] bf16 and e2b [N*k] int64 must be zeroed by the
+ * caller (entries of rank >= mt keep e2b = 0, as in the reference). */
+int ffmoe_routing_scatter_padded(const int64_t* sorted_order, const int64_t* flat_ids,
+                                 const int64_t* starts, const void* x, int64_t N, int D,
+                                 int E, int64_t mt, int k, int64_t n_sorted, void* out,
+                                 int64_t* e2b, void* stream);
 
 #ifdef __cplusplus
 }

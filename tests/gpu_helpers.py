@@ -160,3 +160,34 @@ def moe_reference(x, gate, wu, wd, idx, w, go=None, activation="swiglu", wgrad_e
     res["dgate"] = F_.gemm(gl.t().contiguous(), x)
     res["dwu"], res["dwd"] = dwu, dwd
     return res
+
+
+def exact_expert_wgrads(x, wu, wd, idx, w, go, experts):
+    """fp64 restatement (no intermediate rounding) of the SwiGLU experts'
+    weight gradients for a given routing, for the experts listed: rows of
+    expert e in ascending j = n*k + slot order, up = x w_up[e]^T,
+    act = silu(g) * u, wgo = go[n] * bf16(w[n, slot]) (the combine weights
+    are bf16 on both sides, fused_moe.py:412), gact = wgo w_down[e],
+    dW_down = wgo^T act, dW_up = gup^T x with gup the SwiGLU backward.
+    Returns ({e: dW_up}, {e: dW_down}) in fp64 on x's device."""
+    f = torch.float64
+    N, k = idx.shape
+    H = wd.shape[2]
+    flat = idx.reshape(-1)
+    dwu, dwd = {}, {}
+    for e in experts:
+        j = torch.nonzero(flat == e).flatten()
+        n = j // k
+        xs = x[n].to(f)
+        up = xs @ wu[e].to(f).t()
+        g, u = up[:, :H], up[:, H:]
+        sg = torch.sigmoid(g)
+        act = g * sg * u
+        wgo = go[n].to(f) * w.reshape(-1)[j].to(torch.bfloat16).to(f)[:, None]
+        gact = wgo @ wd[e].to(f)
+        gg = gact * u * (sg * (1.0 + g * (1.0 - sg)))
+        gu = gact * g * sg
+        gup = torch.cat([gg, gu], dim=1)
+        dwd[e] = wgo.t() @ act
+        dwu[e] = gup.t() @ xs
+    return dwu, dwd

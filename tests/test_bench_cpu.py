@@ -19,7 +19,7 @@ def test_bench_refuses_more_than_one_gpu():
 
 
 def test_bench_configs_match_the_baseline_shapes():
-    from flashfusedmoe_amd.bench_configs import CONFIGS
+    from bench_configs import CONFIGS
     with open(os.path.join(ROOT, "BASELINE.json")) as f:
         configs = json.load(f)["configs"]
     # configs[2..4] are C3, C4, C5 in the baseline's own order
@@ -34,7 +34,7 @@ def test_bench_configs_match_the_baseline_shapes():
 
 
 def test_zipf_bias_is_twice_the_log_of_normalised_zipf_weights():
-    from flashfusedmoe_amd.bench_configs import zipf_bias
+    from bench_configs import zipf_bias
     E = 64
     b = zipf_bias(E)
     p = torch.exp(b.double() / 2)

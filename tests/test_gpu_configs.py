@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import check_close, moe_reference
+from gpu_helpers import check_as_accurate, check_close, exact_expert_wgrads, moe_reference
 from oracle import fused as F_
 from oracle import routing as R
 
@@ -94,6 +94,15 @@ def test_c4_skewed_forward_backward():
                     atol=2e-3 * max(1.0, ref["dwu"][e].abs().max().item()))
         check_close(grads[3][e], ref["dwd"][e], f"C4 grad w_down[{e}]",
                     atol=2e-3 * max(1.0, ref["dwd"][e].abs().max().item()))
+    # the max-scaled atol above is paired with an accuracy check: on a sample
+    # of experts (the heaviest included) the GPU's weight gradients are at
+    # least about as close to an fp64 restatement as the bf16 oracle's
+    heavy = int(counts.argmax().item())
+    sample = sorted({heavy, *torch.randperm(E, generator=torch.Generator().manual_seed(44))[:5].tolist()})
+    xdwu, xdwd = exact_expert_wgrads(x, wu, wd, idx, w, go, sample)
+    for e in sample:
+        check_as_accurate(grads[2][e], ref["dwu"][e], xdwu[e], f"C4 grad w_up[{e}] vs fp64")
+        check_as_accurate(grads[3][e], ref["dwd"][e], xdwd[e], f"C4 grad w_down[{e}] vs fp64")
 
 
 def test_c5_deepseek_forward_backward():
@@ -117,6 +126,10 @@ def test_c5_deepseek_forward_backward():
                     atol=2e-3 * max(1.0, ref["dwu"][e].abs().max().item()))
         check_close(grads[3][e], ref["dwd"][e], f"C5 grad w_down[{e}]",
                     atol=2e-3 * max(1.0, ref["dwd"][e].abs().max().item()))
+    xdwu, xdwd = exact_expert_wgrads(x, wu, wd, idx, w, go, sample[:6])
+    for e in sample[:6]:
+        check_as_accurate(grads[2][e], ref["dwu"][e], xdwu[e], f"C5 grad w_up[{e}] vs fp64")
+        check_as_accurate(grads[3][e], ref["dwd"][e], xdwd[e], f"C5 grad w_down[{e}] vs fp64")
 
 
 def test_c5_shared_expert():
@@ -140,3 +153,106 @@ def test_c5_shared_expert():
     ref = F_.gemm(gup.t(), x)
     check_close(dwgu, ref, "C5 shared grad w_gate|w_up",
                 atol=2e-3 * max(1.0, ref.abs().max().item()))
+
+
+def _bench_inputs():
+    """bench.py's exact C2 inputs (seed 0, CPU generator, cast to bf16)."""
+    import bench
+    c = bench.CFG
+    return c, [t.to(torch.bfloat16).cuda() for t in bench.make_inputs(c["N"], c["D"], c["ffn"], c["E"])]
+
+
+def test_c2_layer_forward_backward():
+    """The headline configuration exactly as bench.py times it: fused_moe
+    forward + backward at N 8192, D 1024, ffn 4096, E 8, k 2, swiglu,
+    softmax, aux 0.01, z 1e-3, allow_dropped_tokens=True, the upstream
+    gradients (go, 1) on (out, z_loss).  Routing is bit-exact against the
+    oracle's top-k of the GPU's logits at k = 2; output, losses and all
+    four gradients against the fp32 restatement with the oracle's rounding
+    points plus the z-loss gradient (oracle/fused.py loss_grads); the
+    weight gradients also against fp64 on a sample of experts."""
+    from flashfusedmoe_amd import fused_moe, ops
+    c, (x, gate, wu, wd, go) = _bench_inputs()
+    N, E, k = c["N"], c["E"], c["k"]
+    leaves = [t.clone().requires_grad_(True) for t in (x, gate, wu, wd)]
+    out, losses = fused_moe(*leaves, top_k=k, activation=c["activation"], gating=c["gating"],
+                            aux_loss_coeff=c["aux"], z_loss_coeff=c["z"], allow_dropped_tokens=True)
+    torch.autograd.backward([out, losses["z_loss"]], [go, torch.ones((), device="cuda")])
+    torch.cuda.synchronize()
+    r = ops.route(x, gate, None, k, 0, N * k, 0.0, 0.0, False)
+    logits, idx, w = r[0], r[1], r[2]
+    _check_routing(logits, idx, w, k)
+    lc = logits.cpu()
+    ls = F_.losses(lc, w.cpu(), idx.cpu(), E, aux_loss_coeff=c["aux"], z_loss_coeff=c["z"])
+    torch.testing.assert_close(losses["aux_loss"].cpu(), ls["aux_loss"].float(), rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(losses["z_loss"].cpu(), ls["z_loss"].float(), rtol=1e-4, atol=1e-6)
+    assert not losses["aux_loss"].requires_grad  # softmax aux: no gradient (fused_moe.py:1183-1185)
+
+    ref = moe_reference(x, gate, wu, wd, idx, w, go)
+    lg = F_.loss_grads(lc, idx.cpu(), E, "softmax", c["aux"], c["z"]).to(torch.bfloat16).cuda()
+    check_close(out, ref["out"], "C2 output")
+    check_close(leaves[0].grad, ref["dx"].float() + F_.gemm(lg, gate).float(), "C2 grad hidden")
+    exp_gate = ref["dgate"].float() + F_.gemm(lg.t().contiguous(), x).float()
+    check_close(leaves[1].grad, exp_gate, "C2 grad gate",
+                atol=2e-3 * max(1.0, exp_gate.abs().max().item()))
+    for e in range(E):
+        check_close(leaves[2].grad[e], ref["dwu"][e], f"C2 grad w_up[{e}]",
+                    atol=2e-3 * max(1.0, ref["dwu"][e].abs().max().item()))
+        check_close(leaves[3].grad[e], ref["dwd"][e], f"C2 grad w_down[{e}]",
+                    atol=2e-3 * max(1.0, ref["dwd"][e].abs().max().item()))
+    sample = [0, 5]
+    xdwu, xdwd = exact_expert_wgrads(x, wu, wd, idx, w, go, sample)
+    for e in sample:
+        check_as_accurate(leaves[2].grad[e], ref["dwu"][e], xdwu[e], f"C2 grad w_up[{e}] vs fp64")
+        check_as_accurate(leaves[3].grad[e], ref["dwd"][e], xdwd[e], f"C2 grad w_down[{e}] vs fp64")
+
+
+def test_c2_moelayer_with_shared_expert():
+    """MoELayer(num_shared_experts=1) at C2 (as bench.py builds it: seed 0,
+    bf16 parameters): the routed part against the fp32 restatement, the
+    shared expert against the reference's three bias-free linears
+    (nn.py:22-44) computed with bf16 rounding points, their sum rounded
+    once (nn.py:156-159)."""
+    from flashfusedmoe_amd import MoELayer, ops
+    c, (x, _gate, _wu, _wd, go) = _bench_inputs()
+    N, D, E, k, ffn = c["N"], c["D"], c["E"], c["k"], c["ffn"]
+    torch.manual_seed(0)
+    layer = MoELayer(D, ffn, E, top_k=k, num_shared_experts=1, aux_loss_coeff=c["aux"],
+                     z_loss_coeff=c["z"]).to("cuda", torch.bfloat16)
+    xl = x.clone().requires_grad_(True)
+    out, losses = layer(xl)
+    torch.autograd.backward([out, losses["z_loss"]], [go, torch.ones((), device="cuda")])
+    torch.cuda.synchronize()
+    gate, wu, wd = layer.gate.weight.detach(), layer.w_up.detach(), layer.w_down.detach()
+    se = layer.shared_expert
+    wg, wsu, wsd = se.w_gate.weight.detach(), se.w_up.weight.detach(), se.w_down.weight.detach()
+    r = ops.route(x, gate, None, k, 0, N * k, 0.0, 0.0, False)
+    logits, idx, w = r[0], r[1], r[2]
+    _check_routing(logits, idx, w, k)
+    ref = moe_reference(x, gate, wu, wd, idx, w, go)
+    # shared expert: up = x [w_gate; w_up]^T, act = silu(g) u, down = act w_down^T
+    w_gu = torch.cat([wg, wsu], 0)
+    up = F_.gemm(x, w_gu.t())
+    act = F_.glu_forward(up, "swiglu")
+    sh = F_.gemm(act, wsd.t())
+    check_close(out, (ref["out"].float() + sh.float()).to(torch.bfloat16), "C2 layer output")
+    gup = F_.glu_backward(F_.gemm(go, wsd), up, "swiglu")
+    lg = F_.loss_grads(logits.cpu(), idx.cpu(), E, "softmax", c["aux"], c["z"]).to(torch.bfloat16).cuda()
+    exp_dx = ref["dx"].float() + F_.gemm(lg, gate).float() + F_.gemm(gup, w_gu).float()
+    check_close(xl.grad, exp_dx, "C2 layer grad x")
+    dwgu = F_.gemm(gup.t().contiguous(), x)
+    check_close(se.w_gate.weight.grad, dwgu[: ffn // 2], "C2 shared grad w_gate",
+                atol=2e-3 * max(1.0, dwgu.abs().max().item()))
+    check_close(se.w_up.weight.grad, dwgu[ffn // 2:], "C2 shared grad w_up",
+                atol=2e-3 * max(1.0, dwgu.abs().max().item()))
+    dsd = F_.gemm(go.t().contiguous(), act)
+    check_close(se.w_down.weight.grad, dsd, "C2 shared grad w_down",
+                atol=2e-3 * max(1.0, dsd.abs().max().item()))
+    for e in range(E):
+        check_close(layer.w_up.grad[e], ref["dwu"][e], f"C2 layer grad w_up[{e}]",
+                    atol=2e-3 * max(1.0, ref["dwu"][e].abs().max().item()))
+        check_close(layer.w_down.grad[e], ref["dwd"][e], f"C2 layer grad w_down[{e}]",
+                    atol=2e-3 * max(1.0, ref["dwd"][e].abs().max().item()))
+    exp_gate = ref["dgate"].float() + F_.gemm(lg.t().contiguous(), x).float()
+    check_close(layer.gate.weight.grad, exp_gate, "C2 layer grad gate",
+                atol=2e-3 * max(1.0, exp_gate.abs().max().item()))
