@@ -1,6 +1,7 @@
 // Bandwidth-bound kernels of the fused MoE layer: the weighted top-k combine
 // (and its unweighted backward twin, the dX reduce), the routing backward,
 // the standalone GLU kernels and the padded-layout row scatter.
+#include <mutex>
 #include <string>
 
 #include "common.h"
@@ -727,12 +728,20 @@ extern "C" int64_t ffmoe_gate_grad_workspace_bytes(int64_t N, int D, int E) {
   return ((N + kGateChunk - 1) / kGateChunk) * static_cast<int64_t>(E) * D * 4;
 }
 
-extern "C" int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, int E,
-                               void* workspace, void* dgate, void* stream) {
-  if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_gate_grad: D must be a positive multiple of 8");
-  if (E < 1 || E > FFMOE_MAX_FUSED_GATE_E) return set_error("ffmoe_gate_grad: E out of range");
+static int gate_grad_check(const char* name, int64_t N, int D, int E) {
+  if (N <= 0 || D <= 0 || D % 8 != 0) return set_error(std::string(name) + ": D must be a positive multiple of 8");
+  if (E < 1 || E > FFMOE_MAX_FUSED_GATE_E) return set_error(std::string(name) + ": E out of range");
+  if ((N + kGateChunk - 1) / kGateChunk > 65535)
+    return set_error(std::string(name) + ": N too large (at most 8388480 tokens)");
+  return 0;
+}
+
+// Both passes of the gate-weight gradient with the fp32 partials in
+// `workspace` (ffmoe_gate_grad_workspace_bytes(N, D, E) bytes, every byte
+// written by pass 1 before pass 2 reads it: nothing needs clearing).
+static int gate_grad_launch(const void* gl, const void* x, int64_t N, int D, int E, void* workspace,
+                            void* dgate, void* stream) {
   const int64_t nchunk = (N + kGateChunk - 1) / kGateChunk;
-  if (nchunk > 65535) return set_error("ffmoe_gate_grad: N too large (at most 8388480 tokens)");
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* part = static_cast<float*>(workspace);
   const dim3 grid(static_cast<unsigned>((D + kGateCols - 1) / kGateCols), static_cast<unsigned>(nchunk));
@@ -748,6 +757,51 @@ extern "C" int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, 
                      dim3(256), 0, st, part, nchunk, D, E, static_cast<bf16_t*>(dgate));
   if (check_launch("gate_grad_final_kernel")) return 1;
   return clear_error();
+}
+
+extern "C" int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, int E,
+                               void* workspace, void* dgate, void* stream) {
+  if (gate_grad_check("ffmoe_gate_grad", N, D, E)) return 1;
+  return gate_grad_launch(gl, x, N, D, E, workspace, dgate, stream);
+}
+
+// Scratch of the allocation-free variant: the fp32 partials live in this
+// file-scope device array instead of a caller's workspace.  Each device the
+// library runs on holds its own copy until the process ends; its address on
+// a device comes from hipGetSymbolAddress (the array's name in host code is
+// only a stand-in), looked up once per device on the first call there.
+constexpr int64_t kGateGradScratchBytes = 32ll << 20;
+static __device__ __align__(256) float scratch[kGateGradScratchBytes / 4];
+
+static void* g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+static void* scratch_ptr(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+extern "C" int64_t ffmoe_gate_grad_noalloc_max_bytes(void) { return kGateGradScratchBytes; }
+
+extern "C" int ffmoe_gate_grad_noalloc(const void* gl, const void* x, int64_t N, int D, int E,
+                                       void* dgate, void* stream) {
+  if (gate_grad_check("ffmoe_gate_grad_noalloc", N, D, E)) return 1;
+  const int64_t need = ffmoe_gate_grad_workspace_bytes(N, D, E);
+  if (need > kGateGradScratchBytes)
+    return set_error("ffmoe_gate_grad_noalloc: needs " + std::to_string(need) +
+                     " bytes of scratch (ceil(N/128)*E*D*4); the allocation-free variant holds at most " +
+                     std::to_string(kGateGradScratchBytes) + " (use ffmoe_gate_grad with a workspace)");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return set_error("ffmoe_gate_grad_noalloc: cannot query the current device");
+  void* ptr = scratch_ptr(dev);
+  if (ptr == nullptr) return set_error("ffmoe_gate_grad_noalloc: hipGetSymbolAddress failed for the scratch array");
+  return gate_grad_launch(gl, x, N, D, E, ptr, dgate, stream);
 }
 
 static int route_bwd_impl(const void* go, const void* down, const int32_t* row_of,

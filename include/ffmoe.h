@@ -267,6 +267,19 @@ int64_t ffmoe_gate_grad_workspace_bytes(int64_t N, int D, int E);
 int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, int E,
                     void* workspace, void* dgate, void* stream);
 
+/* ffmoe_gate_grad without a workspace argument and without any allocation:
+ * the fp32 partials live in a device array of
+ * ffmoe_gate_grad_noalloc_max_bytes() bytes (32 MiB) that the library holds
+ * on each device until the process ends.  Problems whose partials need more
+ * (ffmoe_gate_grad_workspace_bytes(N, D, E) > that) are rejected.  Every
+ * call on a device shares that device's array: calls that overlap on one
+ * GPU (different streams or threads) race.  No counterpart in the reference;
+ * it exists for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int64_t ffmoe_gate_grad_noalloc_max_bytes(void);
+int ffmoe_gate_grad_noalloc(const void* gl, const void* x, int64_t N, int D, int E,
+                            void* dgate, void* stream);
+
 /* Routing backward, one pass per token.
  * Replaces: routing-weight grad (fused_moe.py:527-535), `fused_weighted_scatter`
  *   (moe_ops.py:248-332), softmax/sigmoid top-k backward + scatter_add
