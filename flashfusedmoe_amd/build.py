@@ -36,13 +36,37 @@ FLAGS = [
 ]
 
 
+# Kernels whose hand-counted vmcnt waits assume that no scratch (register
+# spill) access ever joins the vector-memory queue: the build fails if the
+# compiler gives any of them scratch.
+NO_SCRATCH_KERNELS = ("gemm_pp_kernel",)
+
+
+def _scratch_kernels(remarks):
+    """Names of kernels with a nonzero ScratchSize in hipcc's
+    -Rpass-analysis=kernel-resource-usage remarks."""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:", 1)[1].split()[0]
+        elif "ScratchSize [bytes/lane]:" in line and name is not None:
+            size = int(line.split("ScratchSize [bytes/lane]:", 1)[1].split()[0])
+            if size > 0 and any(k in name for k in NO_SCRATCH_KERNELS):
+                bad.append(f"{name} ({size} B/lane)")
+    return bad
+
+
 def _compile(unit, objdir):
     src, obj, extra = unit
     obj = os.path.join(objdir, obj)
-    cmd = [HIPCC, *FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *extra, "-Rpass-analysis=kernel-resource-usage", "-c",
+           os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
+    bad = _scratch_kernels(r.stderr)
+    if bad:
+        raise RuntimeError(f"{src}: kernels that must not spill use scratch: {', '.join(bad)}")
     return obj
 
 

@@ -130,6 +130,14 @@ __device__ __forceinline__ void unpack4(uint2 v, float* f) {
 
 // Transpose-read fragment from a swizzled MN-contiguous stage tile [32][R]
 // whose 16-byte chunk c of k-row k sits at chunk c ^ ((k & 3) << 2).
+//
+// The two ds_read_b64_tr_b16 are issued as inline assembly: after a
+// direct-to-LDS buffer load the compiler conservatively puts a vmcnt(0) wait
+// in front of the transpose-read builtin (it cannot tell which LDS bytes the
+// DMA writes), which would make every K step wait for the stage it has just
+// started loading.  The stage the reads target is covered by the K loop's
+// own vmcnt wait and barrier.  The compiler does not track the asm reads'
+// completion: callers wait with lds_frags_ready() before using the result.
 template <int R>
 __device__ __forceinline__ bf16x8_t lds_frag_mn_sw(const bf16_t* t, int c0, int ks, int lane) {
   const int g = lane >> 4, i = lane & 15;
@@ -137,9 +145,40 @@ __device__ __forceinline__ bf16x8_t lds_frag_mn_sw(const bf16_t* t, int c0, int 
   const int col = c0 + (g & 1) * 16 + (i & 3) * 4;
   const int sw = (kb & 3) << 2;  // same for rows kb and kb + 4
   const int off = (((col >> 3) ^ sw) << 3) + (col & 7);
-  const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(t + kb * R + off));
-  const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(t + (kb + 4) * R + off));
-  return bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(t + kb * R + off));
+  typedef unsigned int u32x2v_t __attribute__((ext_vector_type(2)));
+  u32x2v_t lo, hi;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %2\n\t"
+      "ds_read_b64_tr_b16 %1, %2 offset:%3"
+      : "=&v"(lo), "=&v"(hi)
+      : "v"(a0), "i"(4 * R * 2));
+  const bf16x4_t l = __builtin_bit_cast(bf16x4_t, lo), h = __builtin_bit_cast(bf16x4_t, hi);
+  return bf16x8_t{l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
+}
+
+// ds_read_b128 as inline assembly, for K loops whose other fragment reads
+// are asm transpose reads: if the compiler tracked some LDS reads and not
+// others, its own lgkmcnt waits would count the untracked ones too and
+// stall on them.
+__device__ __forceinline__ bf16x8_t lds_read_b128_asm(const bf16_t* p) {
+  typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
+  u32x4v_t v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p))));
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// Waits until every LDS read this wave issued has returned (the asm
+// transpose reads above are not tracked by the compiler) and orders the
+// MFMAs that consume `fa` / `fb` after the wait.  Placed where only those
+// fragments' reads are outstanding, so it costs nothing in steady state.
+template <int NA, int NB>
+__device__ __forceinline__ void lds_frags_ready(bf16x8_t (&fa)[NA], bf16x8_t (&fb)[NB]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < NA; ++i) asm volatile("" : "+v"(fa[i]));
+#pragma unroll
+  for (int i = 0; i < NB; ++i) asm volatile("" : "+v"(fb[i]));
 }
 
 // GLU backward epilogue, split in two so the pre-activation loads can be in
@@ -721,6 +760,13 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   // other.  k-step 0 of stage kt+1 is read right after the barrier that
   // publishes it, during k-step 3 of stage kt.
   bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  // with a transpose-read operand every fragment read is asm (see
+  // lds_read_b128_asm) and lds_frags_ready() does the waiting
+  constexpr bool ASM_READS = !A_KC || !B_KC;
+  auto read_kc = [&](const bf16_t* ptr) {
+    if constexpr (ASM_READS) return lds_read_b128_asm(ptr);
+    else return *reinterpret_cast<const bf16x8_t*>(ptr);
+  };
   auto read_ks = [&](int buf, int ks, bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) {
     const bf16_t* at = smem + buf * STAGE;
     const bf16_t* bt = at + A_EL;
@@ -730,7 +776,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
       if constexpr (A_KC) {
         const int r = r0 + (lane & 31);
         const int c = (ks * 2 + (lane >> 5)) ^ ((r >> 1) & 7);
-        fa[tm] = *reinterpret_cast<const bf16x8_t*>(at + r * DL_BK + c * 8);
+        fa[tm] = read_kc(at + r * DL_BK + c * 8);
       } else {
         fa[tm] = lds_frag_mn_sw<BM>(at, r0, ks, lane);
       }
@@ -741,7 +787,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
       if constexpr (B_KC) {
         const int r = c0 + (lane & 31);
         const int c = (ks * 2 + (lane >> 5)) ^ ((r >> 1) & 7);
-        fb[tn] = *reinterpret_cast<const bf16x8_t*>(bt + r * DL_BK + c * 8);
+        fb[tn] = read_kc(bt + r * DL_BK + c * 8);
       } else {
         fb[tn] = lds_frag_mn_sw<BN>(bt, c0, ks, lane);
       }
@@ -789,17 +835,25 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     read_ks(0, 0, fa0, fb0);
+    // transpose-read operands: wait for a fragment set before its MFMAs
+    auto ready = [&](bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) {
+      if constexpr (!A_KC || !B_KC) lds_frags_ready(fa, fb);
+    };
     int cur = 0;  // ring buffer of the stage being computed
     for (int i = 0; i + 1 < nks; ++i) {
+      ready(fa0, fb0);
       read_ks(cur, 1, fa1, fb1);
       mfma_ks(fa0, fb0);
       interleave(0);
+      ready(fa1, fb1);
       read_ks(cur, 2, fa0, fb0);
       mfma_ks(fa1, fb1);
       interleave(0);
+      ready(fa0, fb0);
       read_ks(cur, 3, fa1, fb1);
       mfma_ks(fa0, fb0);
       interleave(0);
+      ready(fa1, fb1);
       // publish the next stage; every wave's reads of this one have retired
       __builtin_amdgcn_s_waitcnt(kWaitNext);
       asm volatile("" ::: "memory");
@@ -814,12 +868,16 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
       interleave(kLoads);
       cur = nxt;
     }
+    ready(fa0, fb0);
     read_ks(cur, 1, fa1, fb1);
     mfma_ks(fa0, fb0);
+    ready(fa1, fb1);
     read_ks(cur, 2, fa0, fb0);
     mfma_ks(fa1, fb1);
+    ready(fa0, fb0);
     read_ks(cur, 3, fa1, fb1);
     mfma_ks(fa0, fb0);
+    ready(fa1, fb1);
     mfma_ks(fa1, fb1);
   }
   wait_vmcnt_le(0);
