@@ -52,6 +52,9 @@ SIGNATURES = {
     "ffmoe_dx_reduce": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _P, _P]),
     "ffmoe_gate_grad_workspace_bytes": (_L, [_L, _I, _I]),
     "ffmoe_gate_grad": (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
+    "ffmoe_gate_logits_workspace_bytes": (_L, [_L, _I, _I]),
+    "ffmoe_gate_logits": (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
+    "ffmoe_gate_dx": (_I, [_P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_gate_grad_noalloc_max_bytes": (_L, []),
     "ffmoe_gate_grad_noalloc": (_I, [_P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_route_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I,

@@ -725,12 +725,18 @@ extern "C" int ffmoe_dx_reduce(const void* ghb, const int32_t* row_of, const voi
 
 extern "C" int64_t ffmoe_gate_grad_workspace_bytes(int64_t N, int D, int E) {
   if (N <= 0 || D <= 0 || E <= 0) return 0;
+  if (E > FFMOE_MAX_FUSED_GATE_E) {  // MFMA path: one fp32 [E, D] slab per K split
+    const int S = gate_grad_mfma_split(N, D, E);
+    return S > 1 ? static_cast<int64_t>(S) * E * D * 4 : 0;
+  }
   return ((N + kGateChunk - 1) / kGateChunk) * static_cast<int64_t>(E) * D * 4;
 }
 
 static int gate_grad_check(const char* name, int64_t N, int D, int E) {
   if (N <= 0 || D <= 0 || D % 8 != 0) return set_error(std::string(name) + ": D must be a positive multiple of 8");
-  if (E < 1 || E > FFMOE_MAX_FUSED_GATE_E) return set_error(std::string(name) + ": E out of range");
+  if (E < 1 || E > FFMOE_MAX_EXPERTS) return set_error(std::string(name) + ": E out of range");
+  if (E > FFMOE_MAX_FUSED_GATE_E && (E % 8 != 0 || N > 0x7fffffff))
+    return set_error(std::string(name) + ": above 32 experts E must be a multiple of 8");
   if ((N + kGateChunk - 1) / kGateChunk > 65535)
     return set_error(std::string(name) + ": N too large (at most 8388480 tokens)");
   return 0;
@@ -741,6 +747,8 @@ static int gate_grad_check(const char* name, int64_t N, int D, int E) {
 // written by pass 1 before pass 2 reads it: nothing needs clearing).
 static int gate_grad_launch(const void* gl, const void* x, int64_t N, int D, int E, void* workspace,
                             void* dgate, void* stream) {
+  if (E > FFMOE_MAX_FUSED_GATE_E)
+    return gate_grad_mfma(gl, x, N, D, E, workspace, ffmoe_gate_grad_workspace_bytes(N, D, E), dgate, stream);
   const int64_t nchunk = (N + kGateChunk - 1) / kGateChunk;
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* part = static_cast<float*>(workspace);

@@ -26,6 +26,14 @@ int clear_error();
 // Checks hipGetLastError() after a launch; returns 0 or records the failure.
 int check_launch(const char* what);
 
+// The gate-gradient product dgate [E, D] = gl^T x on the MFMA GEMM pipeline
+// (gemm.hip), for expert counts beyond the fused dot2 kernel's: K split over
+// the tokens, fp32 partials (gate_grad_mfma_split(N, D, E) slabs of E*D
+// floats in `workspace`) reduced in a fixed order.
+int gate_grad_mfma_split(int64_t N, int D, int E);
+int gate_grad_mfma(const void* gl, const void* x, int64_t N, int D, int E, void* workspace, int64_t ws_bytes,
+                   void* dgate, void* stream);
+
 __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }

@@ -59,6 +59,7 @@ struct GemmArgs {
   float* part;  // persistent kernel: fp32 partial tiles, one slot per block
   int* flags;   // persistent kernel: one flag per block + an error word
   int lpt;      // wgrad: test the routing skew and balance the tiles over the XCDs
+  int64_t split_rows;  // split-K: rows of one fp32 partial slab
 };
 
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
@@ -575,7 +576,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // is done, the second waits for that publication (its writer is already
 // running, so no co-residency is needed), adds the partial (two terms: the
 // same bits in either order) and runs the epilogue.
-enum Role { ROLE_FULL = 0, ROLE_CUT = 1 };
+// ROLE_SPLIT: one of several K ranges of a tile whose fp32 partials a
+// separate reduction kernel adds up (split-K dense GEMMs): the block writes
+// its accumulators to fp32 slab `slot` ([rows, N] row-major) and is done.
+enum Role { ROLE_FULL = 0, ROLE_CUT = 1, ROLE_SPLIT = 2 };
 
 struct TileCoord {
   int e, m0, n0, row_begin, row_end;
@@ -883,6 +887,28 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord&
   wait_vmcnt_le(0);
   __syncthreads();
 
+  if (role == ROLE_SPLIT) {
+    // row r of the tile holds output row row_begin + r (grouped rows) or
+    // m0 + r (grouped K); slab rows are output rows
+    float* slab = p.part + static_cast<int64_t>(slot) * p.split_rows * p.N;
+    const int rlim = (MODE == 0) ? row_end : p.M;
+    const int rbase = (MODE == 0) ? row_begin : m0;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = rbase + wm * WM + tm * 32 + (lane & 31);
+          const int col = n0 + tile_col(tn) + 8 * q + 4 * (lane >> 5);
+          if (row < rlim && col < p.N)
+            *reinterpret_cast<float4*>(slab + static_cast<int64_t>(row) * p.N + col) =
+                make_float4(acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
+                            acc[tm][tn][4 * q + 3]);
+        }
+    return;
+  }
+
   // cut tile: counter flags[key], publication flags[G + key] (= slot + 1)
   int partner = 0;
   if (role == ROLE_CUT) {
@@ -1081,7 +1107,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
     }
   }
   if (!tc.valid) return;
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
   gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
+#endif
 }
 
 // Persistent grouped-rows GEMM, one block per CU.  The R x n_tiles tiles
@@ -1148,6 +1176,64 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
 template <int BM, int BN, bool A_KC, bool B_KC, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_sk_kernel(GemmArgs p) {
   gemm_sk_body<BM, BN, A_KC, B_KC, EPI>(p);
+}
+
+// Split-K dense GEMM (one row group): block b computes split b % S of tile
+// b / S over its contiguous share of the K steps (grouped rows) or of the
+// rows (grouped K) and writes an fp32 partial slab; split_reduce_kernel adds
+// the S slabs in split order (deterministic) and rounds to bf16 once.
+// Dense GEMM of one row group (no offset tables): grouped rows, C [M, N] =
+// A [M, K] B (MODE 0), or grouped K over all K rows, C [M, N] = A^T B
+// (MODE 1).  With S == 1 each block computes a whole tile and stores bf16;
+// with S > 1 block b computes split b % S of tile b / S over its contiguous
+// share of the K steps and writes an fp32 partial slab, and
+// split_reduce_kernel adds the S slabs in split order (deterministic) and
+// rounds to bf16 once.
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE>
+__global__ __launch_bounds__(kThreads, 1) void gemm_dense_kernel(GemmArgs p, int S) {
+  const int64_t t = blockIdx.x / S;
+  const int s = static_cast<int>(blockIdx.x % S);
+  if (t >= p.total_tiles) return;
+  TileCoord tc{};
+  int mt, nt;
+  grouped_order(t, p.m_tiles, p.n_tiles, &mt, &nt);
+  tc.e = 0;
+  tc.n0 = nt * BN;
+  tc.valid = true;
+  int k0 = 0, k1 = -1;
+  if constexpr (MODE == 0) {
+    tc.row_begin = mt * BM;
+    tc.row_end = p.M;
+    const int nk = p.K / DL_BK;
+    k0 = static_cast<int>(static_cast<int64_t>(nk) * s / S);
+    k1 = static_cast<int>(static_cast<int64_t>(nk) * (s + 1) / S);
+  } else {
+    tc.m0 = mt * BM;
+    // the K rows split into S chunks of whole 64-row steps
+    const int nk = (p.K + DL_BK - 1) / DL_BK;
+    tc.row_begin = static_cast<int>(static_cast<int64_t>(nk) * s / S) * DL_BK;
+    tc.row_end = min(static_cast<int>(static_cast<int64_t>(nk) * (s + 1) / S) * DL_BK, p.K);
+  }
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
+  gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI_STORE>(p, tc, k0, k1, S > 1 ? ROLE_SPLIT : ROLE_FULL, s, 0);
+#endif
+}
+
+// out[i] = bf16(sum_{s < S} part[s][i]) in split order; 4 outputs per thread.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, int S, int64_t n,
+                                                           bf16_t* __restrict__ out) {
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x * 4) {
+    float4 a = *reinterpret_cast<const float4*>(part + i);
+    for (int s = 1; s < S; ++s) {
+      const float4 b = *reinterpret_cast<const float4*>(part + static_cast<int64_t>(s) * n + i);
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+    }
+    *reinterpret_cast<uint2*>(out + i) = make_uint2(pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w));
+  }
 }
 
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
@@ -1365,6 +1451,123 @@ extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t
   a.K = 2 * H;
   return launch_rows<BN, false, EPI_STORE>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
                                            "gemm_dgrad");
+}
+
+// Dense GEMM launch: tiles of BM x BN, the K split S chosen so the grid
+// covers the CUs about once (at most 8 splits, at least 2 K steps each).
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE>
+static int launch_dense(GemmArgs a, void* ws, int64_t ws_bytes, int split, hipStream_t st, const char* name) {
+  a.E = 1;
+  a.b_stride = 0;
+  a.c_stride = 0;
+  a.m_tiles = static_cast<int>((a.M + BM - 1) / BM);
+  a.n_tiles = (a.N + BN - 1) / BN;
+  a.total_tiles = static_cast<int64_t>(a.m_tiles) * a.n_tiles;
+  if (a.total_tiles <= 0 || a.K <= 0) return set_error(std::string(name) + ": empty problem");
+  if (!g_use_tr || (MODE == 0 && a.K % DL_BK != 0))
+    return set_error(std::string(name) + ": K must be a multiple of 64");
+  const int S = split;
+  a.split_rows = a.M;
+  if (S > 1) {
+    const int64_t need = static_cast<int64_t>(S) * a.M * a.N * 4;
+    if (ws == nullptr || ws_bytes < need) return set_error(std::string(name) + ": workspace too small");
+    a.part = static_cast<float*>(ws);
+  }
+  const int64_t grid = a.total_tiles * S;
+  if (grid > 0x7fffffff) return set_error(std::string(name) + ": problem too large");
+  hipLaunchKernelGGL((gemm_dense_kernel<BM, BN, A_KC, B_KC, MODE>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kThreads), 0, st, a, S);
+  if (check_launch(name)) return 1;
+  if (S > 1) {
+    bf16_t* out = a.C;
+    const int64_t n = static_cast<int64_t>(a.M) * a.N;
+    int64_t blocks = (n / 4 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(split_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, a.part, S,
+                       n, out);
+    if (check_launch(name)) return 1;
+  }
+  return clear_error();
+}
+
+// K split for a dense GEMM of `tiles` output tiles and `nk` 64-deep K steps.
+static int dense_split(int64_t tiles, int64_t nk) {
+  const int G = sk_blocks() > 0 ? sk_blocks() : 256;
+  int64_t S = (G + tiles - 1) / tiles;
+  if (S > 8) S = 8;
+  if (S > nk / 2) S = nk / 2;
+  return S < 1 ? 1 : static_cast<int>(S);
+}
+
+static int gate_logits_split(int64_t N, int D, int E) {
+  return dense_split(((N + 255) / 256) * ((E + 127) / 128), D / DL_BK);
+}
+
+namespace ffmoe {
+int gate_grad_mfma_split(int64_t N, int D, int E) {
+  return dense_split(((E + 255) / 256) * static_cast<int64_t>((D + 255) / 256), (N + DL_BK - 1) / DL_BK);
+}
+}  // namespace ffmoe
+
+extern "C" int64_t ffmoe_gate_logits_workspace_bytes(int64_t N, int D, int E) {
+  if (N <= 0 || D <= 0 || E <= 0) return 0;
+  const int S = gate_logits_split(N, D, E);
+  return S > 1 ? static_cast<int64_t>(S) * N * E * 4 : 0;
+}
+
+extern "C" int ffmoe_gate_logits(const void* x, const void* gate, int64_t N, int D, int E, void* logits,
+                                 void* workspace, void* stream) {
+  if (N <= 0 || N > 0x7fffffff || D <= 0 || D % DL_BK != 0 || E < 1 || E > FFMOE_MAX_EXPERTS || E % 8 != 0)
+    return set_error("ffmoe_gate_logits: needs D a multiple of 64 and E a multiple of 8 (at most 256)");
+  GemmArgs a{};
+  a.A = static_cast<const bf16_t*>(x);
+  a.B = static_cast<const bf16_t*>(gate);
+  a.C = static_cast<bf16_t*>(logits);
+  a.lda = D;
+  a.ldb = D;
+  a.ldc = E;
+  a.M = static_cast<int>(N);
+  a.N = E;
+  a.K = D;
+  const int S = gate_logits_split(N, D, E);
+  return launch_dense<256, 128, true, true, 0>(a, workspace, ffmoe_gate_logits_workspace_bytes(N, D, E), S,
+                                               static_cast<hipStream_t>(stream), "ffmoe_gate_logits");
+}
+
+extern "C" int ffmoe_gate_dx(const void* gl, const void* gate, int64_t N, int D, int E, void* out,
+                             void* stream) {
+  if (N <= 0 || N > 0x7fffffff || D <= 0 || D % 8 != 0 || E < 1 || E > FFMOE_MAX_EXPERTS || E % DL_BK != 0)
+    return set_error("ffmoe_gate_dx: needs D a multiple of 8 and E a multiple of 64 (at most 256)");
+  GemmArgs a{};
+  a.A = static_cast<const bf16_t*>(gl);
+  a.B = static_cast<const bf16_t*>(gate);
+  a.C = static_cast<bf16_t*>(out);
+  a.lda = E;
+  a.ldb = D;
+  a.ldc = D;
+  a.M = static_cast<int>(N);
+  a.N = D;
+  a.K = E;
+  return launch_dense<256, 256, true, false, 0>(a, nullptr, 0, 1, static_cast<hipStream_t>(stream),
+                                                "ffmoe_gate_dx");
+}
+
+// dgate [E, D] = gl^T x over all N token rows (the gate-gradient product
+// for expert counts beyond the fused kernel's), split along the tokens.
+int ffmoe::gate_grad_mfma(const void* gl, const void* x, int64_t N, int D, int E, void* workspace,
+                          int64_t ws_bytes, void* dgate, void* stream) {
+  GemmArgs a{};
+  a.A = static_cast<const bf16_t*>(gl);
+  a.B = static_cast<const bf16_t*>(x);
+  a.C = static_cast<bf16_t*>(dgate);
+  a.lda = E;
+  a.ldb = D;
+  a.ldc = D;
+  a.M = E;
+  a.N = D;
+  a.K = static_cast<int>(N);
+  return launch_dense<256, 256, false, false, 1>(a, workspace, ws_bytes, gate_grad_mfma_split(N, D, E),
+                                                 static_cast<hipStream_t>(stream), "ffmoe_gate_grad");
 }
 
 #ifndef FFMOE_WGRAD_LPT_MIN_E

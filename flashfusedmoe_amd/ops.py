@@ -42,11 +42,74 @@ def _check_bf16_gpu(name, t):
 
 # Largest gate matrix (E x D elements) whose GEMM runs inside the route
 # kernel, which streams the whole gate through every 16-token block.  Above
-# it the logits come from one library GEMM (measured routing time, gate GEMM
-# + top-k + scan: 154 -> 109 us at N 16384 / E 64 / D 2048, 1109 -> 312 us
-# at N 4096 / E 256 / D 7168; at E 8 / D 1024 and E 8 / D 4096 the fused
-# kernel is the faster by ~20 us).
+# it the logits come from this library's MFMA gate GEMM (ffmoe_gate_logits)
+# and the route kernel routes them (the fused kernel took 134 us at N 16384 /
+# E 64 / D 2048 and 1099 us at N 4096 / E 256 / D 7168; at E 8 / D 1024 and
+# E 8 / D 4096 it is the faster by ~20 us).
 FUSED_GATE_MAX_ELEMS = 32768
+
+
+def _pad_cols(t, mult):
+    """t [R, C] with its columns zero-padded to a multiple of `mult`."""
+    C = t.shape[1]
+    Cp = -(-C // mult) * mult
+    if Cp == C:
+        return t
+    out = t.new_zeros(t.shape[0], Cp)
+    out[:, :C] = t
+    return out
+
+
+def _pad_rows(t, mult):
+    """t [R, C] with zero rows appended up to a multiple of `mult` rows."""
+    R = t.shape[0]
+    Rp = -(-R // mult) * mult
+    if Rp == R:
+        return t
+    out = t.new_zeros(Rp, t.shape[1])
+    out[:R] = t
+    return out
+
+
+def gate_logits(x, gate):
+    """bf16 logits [N, E] = x gate^T on the MFMA gate GEMM; experts are
+    zero-padded to a multiple of 8 (padded logits are sliced off)."""
+    N, D = x.shape
+    E = gate.shape[0]
+    g = _pad_rows(gate, 8)
+    Ep = g.shape[0]
+    out = torch.empty(N, Ep, dtype=_BF16, device=x.device)
+    ws = torch.empty(max(1, int(L.load().ffmoe_gate_logits_workspace_bytes(N, D, Ep))), dtype=torch.uint8,
+                     device=x.device)
+    L.call("ffmoe_gate_logits", L.ptr(x), L.ptr(g), N, D, Ep, L.ptr(out), L.ptr(ws), L.stream_ptr(x.device))
+    return out if Ep == E else out[:, :E].contiguous()
+
+
+def gate_dx(gl, gate):
+    """bf16 [N, D] = gl gate on the MFMA pipeline; experts zero-padded to a
+    multiple of 64 (zero columns of gl meet zero rows of the gate)."""
+    N, E = gl.shape
+    D = gate.shape[1]
+    glp = _pad_cols(gl, 64)
+    gp = _pad_rows(gate, 64)
+    out = torch.empty(N, D, dtype=_BF16, device=gl.device)
+    L.call("ffmoe_gate_dx", L.ptr(glp), L.ptr(gp), N, D, glp.shape[1], L.ptr(out), L.stream_ptr(gl.device))
+    return out
+
+
+def gate_grad(gl, x):
+    """bf16 dgate [E, D] = gl^T x: the fused dot2 kernel up to 32 experts,
+    the MFMA pipeline above (experts zero-padded to a multiple of 8)."""
+    N, E = gl.shape
+    D = x.shape[1]
+    glp = gl if E <= L.MAX_FUSED_GATE_E else _pad_cols(gl, 8)
+    Ep = glp.shape[1]
+    dgate = torch.empty(Ep, D, dtype=_BF16, device=x.device)
+    part = torch.empty(max(1, int(L.load().ffmoe_gate_grad_workspace_bytes(N, D, Ep))), dtype=torch.uint8,
+                       device=x.device)
+    L.call("ffmoe_gate_grad", L.ptr(glp), L.ptr(x), N, D, Ep, L.ptr(part), L.ptr(dgate),
+           L.stream_ptr(x.device))
+    return dgate if Ep == E else dgate[:E].contiguous()
 
 
 @torch.library.custom_op("ffmoe::route", mutates_args=())
@@ -85,12 +148,12 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
     if noise is not None:
         _check_bf16_gpu("input jitter noise", noise)
     logits_in = None
-    if E * D > FUSED_GATE_MAX_ELEMS:
+    if E * D > FUSED_GATE_MAX_ELEMS and D % 64 == 0:
         # the route kernel streams the whole gate matrix through every
-        # 16-token block; a large gate goes through one library GEMM
-        # (hipBLASLt) and the kernel routes its bf16 logits
+        # 16-token block; a large gate goes through the MFMA gate GEMM and
+        # the kernel routes its bf16 logits
         xin = x if noise is None else x * noise  # bf16(x * noise), as the kernel's jitter
-        logits = torch.matmul(xin, gate.t())
+        logits = gate_logits(xin, gate)
         logits_in, noise = logits, None
     L.call("ffmoe_route_fwd_ex", L.ptr(x), L.ptr(gate), L.ptr(logits_in), L.ptr(bias),
            int(bias_round), int(pre_softmax), float(scoring), int(n_group), int(topk_group),
@@ -247,17 +310,11 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     if fused_gate:  # the gl @ gate term is computed inside the dX reduce
         L.call("ffmoe_dx_reduce", L.ptr(ghb), L.ptr(row_of), L.ptr(gl), L.ptr(gate), N, D, E, k,
                L.ptr(dx), st)
-    else:  # many experts: the dense product is a plain library GEMM (hipBLASLt)
-        addend = torch.matmul(gl, gate)
+    else:  # many experts: gl @ gate on the MFMA pipeline, added by the combine
+        addend = gate_dx(gl, gate)
         L.call("ffmoe_combine", L.ptr(ghb), L.ptr(row_of), None, L.ptr(addend), N, D, k, L.ptr(dx),
                st)
-    if fused_gate:
-        dgate = torch.empty(E, D, dtype=_BF16, device=dev)
-        part = torch.empty(int(L.load().ffmoe_gate_grad_workspace_bytes(N, D, E)), dtype=torch.uint8,
-                           device=dev)
-        L.call("ffmoe_gate_grad", L.ptr(gl), L.ptr(x), N, D, E, L.ptr(part), L.ptr(dgate), st)
-    else:
-        dgate = torch.matmul(gl.t().contiguous(), x)
+    dgate = gate_grad(gl, x)
     if _CHECK_GEMM:
         L.check_gemm_workspaces()
     return [dx, dgate, dwu, dwd]

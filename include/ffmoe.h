@@ -262,10 +262,34 @@ int ffmoe_dx_reduce(const void* ghb, const int32_t* row_of, const void* gl,
 /* Bytes of fp32 partials ffmoe_gate_grad needs for N tokens. */
 int64_t ffmoe_gate_grad_workspace_bytes(int64_t N, int D, int E);
 
-/* dgate [E,D] bf16 = gl^T · x, fp32 accumulation in a fixed order; E <=
- * FFMOE_MAX_FUSED_GATE_E.  Replaces: `gl.t() @ hidden` (fused_moe.py:591). */
+/* dgate [E,D] bf16 = gl^T · x, fp32 accumulation in a fixed order.  Up to
+ * FFMOE_MAX_FUSED_GATE_E experts a token-chunked bf16 dot2 kernel; above
+ * that (E a multiple of 8, at most 256) the MFMA GEMM pipeline with the
+ * token dimension split across blocks and the fp32 partials reduced in
+ * split order.  Replaces: `gl.t() @ hidden` (fused_moe.py:591). */
 int ffmoe_gate_grad(const void* gl, const void* x, int64_t N, int D, int E,
                     void* workspace, void* dgate, void* stream);
+
+/* Bytes of fp32 partials ffmoe_gate_logits needs (0 when it does not split
+ * the reduction). */
+int64_t ffmoe_gate_logits_workspace_bytes(int64_t N, int D, int E);
+
+/* logits [N,E] bf16 = x [N,D] · gate [E,D]^T on the MFMA GEMM pipeline (fp32
+ * accumulation; the D reduction split across blocks when the tiles alone do
+ * not fill the GPU, fp32 partials reduced in split order, one bf16 rounding).
+ * D a multiple of 64, E a multiple of 8 (at most 256).  For gate matrices
+ * too large for the route kernel's own gate GEMM, whose logits are then
+ * passed to ffmoe_route_fwd as logits_in.
+ * Replaces: the gate GEMM `hidden @ gate.T` (fused_moe.py:334, :1165). */
+int ffmoe_gate_logits(const void* x, const void* gate, int64_t N, int D, int E,
+                      void* logits, void* workspace, void* stream);
+
+/* out [N,D] bf16 = gl [N,E] · gate [E,D] on the MFMA GEMM pipeline (fp32
+ * accumulation, one bf16 rounding); E a multiple of 64 (at most 256), D a
+ * multiple of 8.  The addend of ffmoe_combine for the dX reduce above
+ * FFMOE_MAX_FUSED_GATE_E experts.  Replaces: `gl @ gate` (fused_moe.py:590). */
+int ffmoe_gate_dx(const void* gl, const void* gate, int64_t N, int D, int E,
+                  void* out, void* stream);
 
 /* ffmoe_gate_grad without a workspace argument and without any allocation:
  * the fp32 partials live in a device array of

@@ -273,8 +273,67 @@ def test_dx_reduce_and_gate_grad_against_fp32(E, _lib):
     check_close(dgate.cpu(), gl.double().t() @ x.double(), "dgate")
 
 
-def test_many_experts_gate_products_use_library_path():
-    # E above the fused-kernel limit: gl @ gate and gl^T x go to hipBLASLt
+@pytest.mark.parametrize("N,D,E", [(1000, 256, 48), (4096, 1024, 64), (700, 7168, 256), (333, 64, 40)])
+def test_mfma_gate_products_against_fp64(N, D, E):
+    """Above 32 experts gl @ gate (ffmoe_gate_dx) and gl^T x
+    (ffmoe_gate_grad's MFMA split-K path) run on the MFMA GEMM pipeline with
+    fp32 accumulation and one bf16 rounding: within one bf16 ulp of the
+    exact product plus the fp32 summation bound, and at most 2% of them not
+    the correctly rounded value.  E = 40 and 48 exercise the zero padding."""
+    from flashfusedmoe_amd import ops
+    g = torch.Generator().manual_seed(N + E)
+    gl = (torch.randn(N, E, generator=g) * 0.1).to(torch.bfloat16)
+    gate = (torch.randn(E, D, generator=g) * 0.05).to(torch.bfloat16)
+    x = torch.randn(N, D, generator=g).to(torch.bfloat16)
+    dx = ops.gate_dx(gl.cuda(), gate.cuda()).cpu()
+    dgate = ops.gate_grad(gl.cuda(), x.cuda()).cpu()
+    for name, got, a, b in (("gl @ gate", dx, gl.double(), gate.double()),
+                            ("gl^T x", dgate, gl.double().t(), x.double())):
+        exact = a @ b
+        absum = a.abs() @ b.abs()
+        ulp = torch.exp2(torch.floor(torch.log2(exact.abs().clamp_min(1e-30))) - 7)
+        err = (got.double() - exact).abs()
+        assert bool((err <= ulp + 2.0 ** -20 * absum).all()), f"{name} outside the rounding bound"
+        assert (got != exact.to(torch.bfloat16)).double().mean().item() < 0.02, name
+
+
+@pytest.mark.parametrize("N,D,E", [(16384, 2048, 64), (4096, 7168, 256), (1000, 512, 100)])
+def test_mfma_gate_logits_split_k(N, D, E):
+    """The MFMA gate GEMM (split along D, fp32 partials added in a fixed
+    order): within the rounding bound of the exact product, almost always the
+    correctly rounded bf16, bitwise repeatable.  Also reports how many
+    logits are not the correctly rounded value and how many tokens' top-k
+    differ from routing the exact logits (ties of nearly equal logits)."""
+    from flashfusedmoe_amd import ops
+    x, gate, _, _ = seeded(N, D, 16, E, seed=N + D + E)
+    lg = ops.gate_logits(x.cuda(), gate.cuda())
+    lg2 = ops.gate_logits(x.cuda(), gate.cuda())
+    assert torch.equal(lg, lg2)
+    lg = lg.cpu()
+    exact64 = x.double() @ gate.double().t()
+    absum = x.double().abs() @ gate.double().abs().t()
+    ulp = torch.exp2(torch.floor(torch.log2(exact64.abs().clamp_min(1e-30))) - 7)
+    err = (lg.double() - exact64).abs()
+    assert bool((err <= ulp + 2.0 ** -20 * absum).all()), "logits outside the rounding bound"
+    not_rounded = (lg != exact64.to(torch.bfloat16)).double().mean().item()
+    assert not_rounded < 0.02
+    k = 8
+    _, idx_gpu = R.route(lg.float().numpy(), k)
+    # what an exact GEMM hands the router: the correctly rounded bf16 logits
+    _, idx_rn = R.route(exact64.to(torch.bfloat16).float().numpy(), k)
+    _, idx_exact = R.route(exact64.float().numpy(), k)
+    differ = int((idx_gpu != idx_rn).any(axis=1).sum())
+    differ_exact = int((idx_gpu != idx_exact).any(axis=1).sum())
+    print(f"\n[parity report] N={N} D={D} E={E}: {not_rounded:.4%} of logits not the correctly "
+          f"rounded bf16; {differ} of {N} tokens route differently from the correctly rounded "
+          f"logits' top-{k} ({differ_exact} from the unrounded fp64 logits' top-{k}, where bf16 "
+          f"ties are broken by value)")
+    assert differ <= 0.002 * N
+
+
+def test_many_experts_gate_products_use_mfma_path():
+    # E above the fused-kernel limit: gl @ gate and gl^T x run on the MFMA
+    # pipeline (ffmoe_gate_dx, ffmoe_gate_grad's split-K path)
     N, D, ffn, E, k = 512, 128, 256, 64, 4
     x, gate, wu, wd = seeded(N, D, ffn, E, seed=64)
     go = torch.randn(N, D, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
