@@ -114,11 +114,40 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
   const int ntok = static_cast<int>(min<int64_t>(kRouteTokens, N - tok_base));
 
   if constexpr (FROM_LOGITS) {
-    for (int p = tid; p < kRouteTokens * EP; p += kRouteThreads) {
-      const int t = p / EP, e = p % EP;
-      bf16_t v = 0;
-      if (t < ntok && e < E) v = logits_in[(tok_base + t) * E + e];
-      L[t * LS + e] = v;
+    if (E % 8 == 0) {
+      // 16-byte loads, all of a thread's in flight before the first LDS
+      // write (logits rows are 16-byte aligned when E % 8 == 0; the LDS
+      // rows, padded by 4 bytes, take them as four 4-byte writes)
+      constexpr int NV = kRouteTokens * EP / 8;
+      constexpr int PER = (NV + kRouteThreads - 1) / kRouteThreads;
+      uint4 v[PER];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int p = i * kRouteThreads + tid;
+        const int t = p / (EP / 8), e = (p % (EP / 8)) * 8;
+        v[i] = make_uint4(0, 0, 0, 0);
+        if (p < NV && t < ntok && e < E)
+          v[i] = *reinterpret_cast<const uint4*>(logits_in + (tok_base + t) * E + e);
+      }
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int p = i * kRouteThreads + tid;
+        const int t = p / (EP / 8), e = (p % (EP / 8)) * 8;
+        if (p < NV) {
+          uint32_t* d = reinterpret_cast<uint32_t*>(L + t * LS + e);
+          d[0] = v[i].x;
+          d[1] = v[i].y;
+          d[2] = v[i].z;
+          d[3] = v[i].w;
+        }
+      }
+    } else {
+      for (int p = tid; p < kRouteTokens * EP; p += kRouteThreads) {
+        const int t = p / EP, e = p % EP;
+        bf16_t v = 0;
+        if (t < ntok && e < E) v = logits_in[(tok_base + t) * E + e];
+        L[t * LS + e] = v;
+      }
     }
   } else {
     // Wave `wave` computes logits of tokens [16*wave, 16*wave+16) against all
@@ -223,6 +252,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     // logsumexp of the logits (z-loss and the pre-softmax probabilities)
     float m = -INFINITY, s = 0.0f;
     if (tok_ok) {
+#pragma unroll 8
       for (int e = jl; e < E; e += LPT) {
         const float l = bf16_to_f32(lr[e]);
         if (l > m) {
@@ -303,8 +333,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
         }
       }
     } else {
-      if (tok_ok)
+      if (tok_ok) {
+#pragma unroll 4
         for (int e = jl; e < E; e += LPT) tk.push(score(e), e, k);
+      }
 #pragma unroll
       for (int off = 1; off < LPT; off <<= 1) {
         float pv[KMAX];
