@@ -48,6 +48,11 @@ SIGNATURES = {
     "ffmoe_gemm_dgrad_glu": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
     "ffmoe_gemm_dgrad": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P]),
     "ffmoe_gemm_wgrad": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
+    "ffmoe_gemm_up_glu_shared": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "ffmoe_gemm_down_shared": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P, _P]),
+    "ffmoe_gemm_dgrad_glu_shared": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P, _P]),
+    "ffmoe_gemm_dgrad_shared": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P, _P]),
+    "ffmoe_gemm_wgrad_shared": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _P]),
     "ffmoe_combine": (_I, [_P, _P, _P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_dx_reduce": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _P, _P]),
     "ffmoe_gate_grad_workspace_bytes": (_L, [_L, _I, _I]),
@@ -66,6 +71,18 @@ SIGNATURES = {
     "ffmoe_scatter_rows": (_I, [_P, _P, _P, _L, _I, _I, _L, _P, _P]),
     "ffmoe_routing_scatter_padded": (_I, [_P, _P, _P, _P, _L, _I, _I, _L, _I, _L, _P, _P, _P]),
 }
+
+class DenseGroup(ctypes.Structure):
+    """ffmoe_dense_group (include/ffmoe.h): a dense row group computed in
+    the same launch as the routed experts (MoELayer's shared expert)."""
+    _fields_ = [("a", _P), ("b", _P), ("up", _P), ("c", _P), ("c2", _P), ("rows", _L),
+                ("activation", _I)]
+
+
+def dense_group(a, b, c, rows, activation, up=None, c2=None):
+    """A DenseGroup over tensors (None -> NULL); pass it with ctypes.byref."""
+    return DenseGroup(ptr(a), ptr(b), ptr(up), ptr(c), ptr(c2), int(rows), int(activation))
+
 
 _lib = None
 _lock = threading.Lock()

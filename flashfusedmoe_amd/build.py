@@ -36,47 +36,76 @@ FLAGS = [
 ]
 
 
-# Kernels whose hand-counted vmcnt waits assume that no scratch (register
-# spill) access ever joins the vector-memory queue: the build fails if the
-# compiler gives any of them scratch.
-NO_SCRATCH_KERNELS = ("gemm_pp_kernel",)
+# The grouped GEMMs count their outstanding vector-memory operations by hand
+# (s_waitcnt vmcnt(N) with N > 0 after the direct-to-LDS operand loads).  A
+# register spill placed between such a load and such a wait would join the
+# counted sequence and let the wait pass early, so every build checks the
+# device assembly of gemm.hip for that pattern and fails if it finds one.
+CHECKED_ASM = ("gemm.hip",)
 
 
-def _scratch_kernels(remarks):
-    """Names of kernels with a nonzero ScratchSize in hipcc's
-    -Rpass-analysis=kernel-resource-usage remarks."""
-    bad, name = [], None
-    for line in remarks.splitlines():
-        if "Function Name:" in line:
-            name = line.split("Function Name:", 1)[1].split()[0]
-        elif "ScratchSize [bytes/lane]:" in line and name is not None:
-            size = int(line.split("ScratchSize [bytes/lane]:", 1)[1].split()[0])
-            if size > 0 and any(k in name for k in NO_SCRATCH_KERNELS):
-                bad.append(f"{name} ({size} B/lane)")
-    return bad
+def unsafe_scratch_ops(asm_text):
+    """(kernel, wait, line) for every scratch access that lies, in
+    straight-line code, between a direct-to-LDS buffer load and a later
+    s_waitcnt vmcnt(N > 0) with no vmcnt(0) wait, label or branch between
+    them."""
+    import re
+    out = []
+    kernel, seen_dma, scratch = None, False, []
+    for i, line in enumerate(asm_text.splitlines()):
+        t = line.strip()
+        m = re.match(r"^(_Z\S+):", line)
+        if m:
+            kernel, seen_dma, scratch = m.group(1), False, []
+        elif t.startswith(".L") or t.startswith("s_branch") or t.startswith("s_cbranch"):
+            seen_dma, scratch = False, []
+        elif "offen lds" in t:
+            seen_dma, scratch = True, []
+        elif "scratch_" in t and seen_dma:
+            scratch.append(i)
+        elif t.startswith("s_waitcnt") and "vmcnt(" in t:
+            n = int(re.search(r"vmcnt\((\d+)\)", t).group(1))
+            if n > 0:
+                out.extend((kernel, t, j) for j in scratch)
+            else:
+                seen_dma, scratch = False, []
+    return out
 
 
 def _compile(unit, objdir):
     src, obj, extra = unit
     obj = os.path.join(objdir, obj)
-    cmd = [HIPCC, *FLAGS, *extra, "-Rpass-analysis=kernel-resource-usage", "-c",
-           os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
-    bad = _scratch_kernels(r.stderr)
-    if bad:
-        raise RuntimeError(f"{src}: kernels that must not spill use scratch: {', '.join(bad)}")
     return obj
+
+
+def _check_asm(src, objdir):
+    out = os.path.join(objdir, src.replace(".hip", ".s"))
+    cmd = [HIPCC, *FLAGS, "--cuda-device-only", "-S", "-c", os.path.join(CSRC, src), "-o", out]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {src}:\n{r.stderr}")
+    with open(out) as f:
+        bad = unsafe_scratch_ops(f.read())
+    os.remove(out)
+    if bad:
+        names = sorted({k for k, _, _ in bad})
+        raise RuntimeError(f"{src}: register spills inside hand-counted vmcnt sequences in {names}")
 
 
 def build(verbose=True):
     """Compiles every source and links libffmoe.so next to this file."""
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    jobs = max(1, min(len(UNITS), int(os.environ.get("MAX_JOBS", "8"))))
+    jobs = max(1, min(len(UNITS) + len(CHECKED_ASM), int(os.environ.get("MAX_JOBS", "8"))))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
+        checks = [ex.submit(_check_asm, src, objdir) for src in CHECKED_ASM]
         objs = list(ex.map(lambda u: _compile(u, objdir), UNITS))
+        for c in checks:
+            c.result()
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)

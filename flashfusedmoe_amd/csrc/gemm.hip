@@ -60,7 +60,24 @@ struct GemmArgs {
   int* flags;   // persistent kernel: one flag per block + an error word
   int lpt;      // wgrad: test the routing skew and balance the tiles over the XCDs
   int64_t split_rows;  // split-K: rows of one fp32 partial slab
+  // An optional dense row group after the routed experts (the shared expert
+  // of MoELayer): its own operands and outputs, x_rows rows, activation
+  // x_act.  Grouped rows: rows [0, x_rows) of xA against xB; grouped K: the
+  // (E+1)-th group, K = x_rows rows of xA and xB, output xC.
+  const bf16_t* xA;
+  const bf16_t* xB;
+  bf16_t* xC;
+  bf16_t* xC2;
+  const bf16_t* xUp;
+  int x_rows;
+  int x_act;
 };
+
+// Row tiles of the extra dense group.
+template <int BM>
+__device__ __forceinline__ int extra_tiles(const GemmArgs& p) {
+  return p.x_rows > 0 ? (p.x_rows + BM - 1) / BM : 0;
+}
 
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
   // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
@@ -584,6 +601,7 @@ enum Role { ROLE_FULL = 0, ROLE_CUT = 1, ROLE_SPLIT = 2 };
 struct TileCoord {
   int e, m0, n0, row_begin, row_end;
   bool valid;
+  bool extra;  // a tile of the extra dense group
 };
 
 // Row-group tables are read through the constant address space: they do not
@@ -601,8 +619,16 @@ __device__ __forceinline__ TileCoord decode_rows_tile(const GemmArgs& p, int64_t
   int mt, nt;
   grouped_order(t, m_count, p.n_tiles, &mt, &nt);
   c.n0 = nt * BN;
-  c.valid = mt < ld_const(p.tile_offsets, p.E);
+  const int R = ld_const(p.tile_offsets, p.E);
+  c.valid = mt < R + extra_tiles<BM>(p);
   if (!c.valid) return c;
+  if (mt >= R) {  // the extra dense group's row tiles follow the routed ones
+    c.extra = true;
+    c.e = 0;
+    c.row_begin = (mt - R) * BM;
+    c.row_end = p.x_rows;
+    return c;
+  }
   int lo = 0, hi = p.E - 1;  // last e with tile_offsets[e] <= mt
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -624,9 +650,16 @@ __device__ __forceinline__ TileCoord decode_k_tile(const GemmArgs& p, int64_t t)
   grouped_order(t - static_cast<int64_t>(c.e) * per_e, p.m_tiles, p.n_tiles, &mt, &nt);
   c.m0 = mt * BM;
   c.n0 = nt * BN;
+  c.valid = true;
+  if (c.e >= p.E) {  // the extra dense group: all of its rows
+    c.extra = true;
+    c.e = 0;
+    c.row_begin = 0;
+    c.row_end = p.x_rows;
+    return c;
+  }
   c.row_begin = ld_const(p.offsets, c.e);
   c.row_end = ld_const(p.offsets, c.e + 1);
-  c.valid = true;
   return c;
 }
 
@@ -638,8 +671,20 @@ constexpr int kDeviceScope = 16;
 // __device__ function (the buffer-descriptor type exists only in the device
 // pass); the kernels below loop over tiles with it.
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
-__device__ __forceinline__ void gemm_dl_tile(const GemmArgs& p, const TileCoord& tc, int k0, int k1,
+__device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord& tc, int k0, int k1,
                                              int role, int slot, int key) {
+  // a tile of the extra dense group reads and writes its own tensors
+  GemmArgs p = pa;
+  if (tc.extra) {
+    p.A = pa.xA;
+    p.B = pa.xB;
+    p.C = pa.xC;
+    p.C2 = pa.xC2;
+    p.up = pa.xUp;
+    p.act = pa.x_act;
+    p.b_stride = 0;
+    p.c_stride = 0;
+  }
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int A_EL = BM * DL_BK, B_EL = BN * DL_BK;  // elements per stage tile
@@ -1037,7 +1082,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
     // x, x + 8, ...).  The grid covers an upper bound of row tiles; the R
     // real ones (known on the device) are split evenly, each XCD taking a
     // contiguous run, so no XCD runs a round more than the others.
-    const int R = ld_const(p.tile_offsets, p.E);
+    const int R = ld_const(p.tile_offsets, p.E) + extra_tiles<BM>(p);
     const int64_t T = static_cast<int64_t>(R) * p.n_tiles;
     const int64_t per = (T + 7) / 8;
     const int64_t idx = blockIdx.x >> 3;
@@ -1060,41 +1105,44 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
       // same decision (one ballot), so the test needs no block barrier.
       // Loads go out four per lane at a time (clamped in range) before any
       // is waited for.
-      const int64_t total3 = 3 * static_cast<int64_t>(p.offsets[p.E] - p.offsets[0]);
+      // the extra dense group (if any) is group E, with x_rows rows
+      const int NG = p.E + (p.x_rows > 0 ? 1 : 0);
+      const int64_t total3 = 3 * (static_cast<int64_t>(p.offsets[p.E] - p.offsets[0]) + (p.x_rows > 0 ? p.x_rows : 0));
       bool heavy = false;
-      for (int i0 = threadIdx.x & 63; i0 < p.E; i0 += 256) {
-        int lo[4], hi[4];
+      for (int i0 = threadIdx.x & 63; i0 < NG; i0 += 256) {
+        int cnt[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int i = min(i0 + 64 * u, p.E - 1);
-          lo[u] = p.offsets[i];
-          hi[u] = p.offsets[i + 1];
+          const int i = min(i0 + 64 * u, NG - 1);
+          cnt[u] = i < p.E ? p.offsets[min(i, p.E - 1) + 1] - p.offsets[min(i, p.E - 1)] : p.x_rows;
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-          heavy |= i0 + 64 * u < p.E && 2 * static_cast<int64_t>(hi[u] - lo[u]) * p.E >= total3;
+          heavy |= i0 + 64 * u < NG && 2 * static_cast<int64_t>(cnt[u]) * NG >= total3;
       }
       skewed = __ballot(heavy && total3 > 0) != 0;
     }
     if (skewed) {
       // Every XCD takes a contiguous slice of ceil(per_e / 8) tiles of every
-      // expert, and the experts are visited heaviest first (ties: lower
+      // group, and the groups are visited heaviest first (ties: lower
       // index first), so the long tiles start at once and the short ones
       // fill in behind them.
-      __shared__ int s_cnt[kLptMaxE];
+      __shared__ int s_cnt[kLptMaxE + 1];
       __shared__ int s_sel;
+      const int NG = p.E + (p.x_rows > 0 ? 1 : 0);
       const int per_e = p.m_tiles * p.n_tiles;
       const int c = (per_e + 7) / 8;
       const int sl = static_cast<int>(blockIdx.x >> 3);
-      const int r = sl / c;                                           // rank of the expert
+      const int r = sl / c;                                           // rank of the group
       const int sub = static_cast<int>(blockIdx.x & 7) * c + sl % c;  // its tile
-      if (r >= p.E || sub >= per_e) return;
-      for (int i = threadIdx.x; i < p.E; i += kThreads) s_cnt[i] = p.offsets[i + 1] - p.offsets[i];
+      if (r >= NG || sub >= per_e) return;
+      for (int i = threadIdx.x; i < NG; i += kThreads)
+        s_cnt[i] = i < p.E ? p.offsets[i + 1] - p.offsets[i] : p.x_rows;
       __syncthreads();
-      for (int i = threadIdx.x; i < p.E; i += kThreads) {
+      for (int i = threadIdx.x; i < NG; i += kThreads) {
         const int ci = s_cnt[i];
         int rank = 0;
-        for (int j = 0; j < p.E; ++j) {
+        for (int j = 0; j < NG; ++j) {
           const int cj = s_cnt[j];
           rank += (cj > ci) || (cj == ci && j < i);
         }
@@ -1125,7 +1173,7 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& p) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
   const int G = gridDim.x;
   const int v = (G % 8 == 0) ? static_cast<int>(xcd_remap(blockIdx.x, G)) : static_cast<int>(blockIdx.x);
-  const int R = ld_const(p.tile_offsets, p.E);
+  const int R = ld_const(p.tile_offsets, p.E) + extra_tiles<BM>(p);
   const int64_t T = static_cast<int64_t>(R) * p.n_tiles;
   const int nk = p.K / DL_BK;
   if (T == 0 || nk == 0) return;
@@ -1242,7 +1290,10 @@ static int launch(const GemmArgs& a, hipStream_t st, const char* name) {
   // the direct-to-LDS pipeline needs whole K steps (grouped-rows mode) and the
   // transpose-read path; everything else takes the register-staged kernel
   const bool dl = g_use_tr && (MODE == 1 || a.K % DL_BK == 0);
-  const int64_t grid = (dl && a.lpt) ? static_cast<int64_t>(a.E) * 8 * ((a.m_tiles * a.n_tiles + 7) / 8)
+  if (a.x_rows > 0 && !dl)
+    return set_error(std::string(name) + ": a dense extra group needs K a multiple of 64 and the transpose-read path");
+  const int groups = a.E + (a.x_rows > 0 ? 1 : 0);
+  const int64_t grid = (dl && a.lpt) ? static_cast<int64_t>(groups) * 8 * ((a.m_tiles * a.n_tiles + 7) / 8)
                                      : (a.total_tiles + 7) / 8 * 8;
   if (grid > 0x7fffffff) return set_error(std::string(name) + ": problem too large");
   if (dl)
@@ -1315,6 +1366,25 @@ static GemmArgs rows_args(const int32_t* offsets, const int32_t* tile_offsets, i
   return a;
 }
 
+// Adds the extra dense group to grouped-rows arguments (its row tiles after
+// the routed ones).
+static int apply_shared(GemmArgs& a, const ffmoe_dense_group* g, int tile_rows, const char* name) {
+  if (g == nullptr || g->rows <= 0) return 0;
+  if (g->a == nullptr || g->b == nullptr || g->c == nullptr || g->rows > 0x7fffffff ||
+      g->activation < 0 || g->activation > FFMOE_ACT_GEGLU_ERF)
+    return set_error(std::string(name) + ": bad dense extra group");
+  a.xA = static_cast<const bf16_t*>(g->a);
+  a.xB = static_cast<const bf16_t*>(g->b);
+  a.xC = static_cast<bf16_t*>(g->c);
+  a.xC2 = static_cast<bf16_t*>(g->c2);
+  a.xUp = static_cast<const bf16_t*>(g->up);
+  a.x_rows = static_cast<int>(g->rows);
+  a.x_act = g->activation;
+  a.m_tiles += static_cast<int>((g->rows + tile_rows - 1) / tile_rows);
+  a.total_tiles = static_cast<int64_t>(a.m_tiles) * a.n_tiles;
+  return 0;
+}
+
 static int check_rows(const char* name, int E, int64_t max_rows, int D, int H, int tile_rows) {
   if (E < 1 || E > FFMOE_MAX_EXPERTS || D <= 0 || D % 8 != 0 || H <= 0 || H % 8 != 0 || max_rows < 0)
     return set_error(std::string(name) + ": D and H must be positive multiples of 8");
@@ -1365,10 +1435,10 @@ extern "C" int ffmoe_set_lds_transpose(int enable) {
   return prev;
 }
 
-extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const int32_t* offsets,
-                                 const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
-                                 int D, int H, int activation, void* up_out, void* act_out,
-                                 void* sk_workspace, void* stream) {
+extern "C" int ffmoe_gemm_up_glu_shared(const void* x_sorted, const void* w_up, const int32_t* offsets,
+                                        const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                                        int D, int H, int activation, void* up_out, void* act_out,
+                                        const ffmoe_dense_group* shared, void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_up_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_gemm_up_glu: unknown activation");
   constexpr int BN = 256;
@@ -1385,15 +1455,25 @@ extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const i
   a.K = D;
   a.H = H;
   a.act = activation;
+  if (apply_shared(a, shared, tile_rows, "ffmoe_gemm_up_glu")) return 1;
   // 256 x 256 tiles, K = D: stream-K only for long K (its cut-tile partials
   // cost more than the whole-tile tail round at D = 1024, measured)
   return launch_rows<BN, true, EPI_GLU_FWD>(a, tile_rows, sk_workspace, kSkMinK,
                                             static_cast<hipStream_t>(stream), "gemm_up_glu");
 }
 
-extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
-                               const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
-                               int H, int D, void* down_out, void* sk_workspace, void* stream) {
+extern "C" int ffmoe_gemm_up_glu(const void* x_sorted, const void* w_up, const int32_t* offsets,
+                                 const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                                 int D, int H, int activation, void* up_out, void* act_out,
+                                 void* sk_workspace, void* stream) {
+  return ffmoe_gemm_up_glu_shared(x_sorted, w_up, offsets, tile_offsets, tile_rows, E, max_rows, D, H,
+                                  activation, up_out, act_out, nullptr, sk_workspace, stream);
+}
+
+extern "C" int ffmoe_gemm_down_shared(const void* act, const void* w_down, const int32_t* offsets,
+                                      const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                                      int H, int D, void* down_out, const ffmoe_dense_group* shared,
+                                      void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_down", E, max_rows, D, H, tile_rows)) return 1;
   constexpr int BN = 128;  // 256 x 128 tiles: a three-stage LDS ring fits
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
@@ -1406,14 +1486,23 @@ extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_
   a.b_stride = static_cast<int64_t>(D) * H;
   a.N = D;
   a.K = H;
+  if (apply_shared(a, shared, tile_rows, "ffmoe_gemm_down")) return 1;
   return launch_rows<BN, true, EPI_STORE>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
                                           "gemm_down");
 }
 
-extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,
-                                    const int32_t* offsets, const int32_t* tile_offsets,
-                                    int tile_rows, int E, int64_t max_rows, int D, int H,
-                                    int activation, void* gup_out, void* sk_workspace, void* stream) {
+extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_t* offsets,
+                               const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                               int H, int D, void* down_out, void* sk_workspace, void* stream) {
+  return ffmoe_gemm_down_shared(act, w_down, offsets, tile_offsets, tile_rows, E, max_rows, H, D, down_out,
+                                nullptr, sk_workspace, stream);
+}
+
+extern "C" int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, const void* up,
+                                           const int32_t* offsets, const int32_t* tile_offsets,
+                                           int tile_rows, int E, int64_t max_rows, int D, int H,
+                                           int activation, void* gup_out, const ffmoe_dense_group* shared,
+                                           void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
   constexpr int BN = 128;  // 256 x 128 tiles: a three-stage LDS ring fits
@@ -1430,13 +1519,25 @@ extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const v
   a.K = D;
   a.H = H;
   a.act = activation;
+  if (shared != nullptr && shared->rows > 0 && shared->up == nullptr)
+    return set_error("ffmoe_gemm_dgrad_glu: the dense extra group needs its pre-activation");
+  if (apply_shared(a, shared, tile_rows, "ffmoe_gemm_dgrad_glu")) return 1;
   return launch_rows<BN, false, EPI_GLU_BWD>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
                                              "gemm_dgrad_glu");
 }
 
-extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t* offsets,
-                                const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
-                                int H, int D, void* ghb_out, void* sk_workspace, void* stream) {
+extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,
+                                    const int32_t* offsets, const int32_t* tile_offsets,
+                                    int tile_rows, int E, int64_t max_rows, int D, int H,
+                                    int activation, void* gup_out, void* sk_workspace, void* stream) {
+  return ffmoe_gemm_dgrad_glu_shared(wgo, w_down, up, offsets, tile_offsets, tile_rows, E, max_rows, D, H,
+                                     activation, gup_out, nullptr, sk_workspace, stream);
+}
+
+extern "C" int ffmoe_gemm_dgrad_shared(const void* gup, const void* w_up, const int32_t* offsets,
+                                       const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                                       int H, int D, void* ghb_out, const ffmoe_dense_group* shared,
+                                       void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad", E, max_rows, D, H, tile_rows)) return 1;
   constexpr int BN = 256;  // 256 x 256 tiles (two stages) under the stream-K schedule
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
@@ -1449,8 +1550,16 @@ extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t
   a.b_stride = static_cast<int64_t>(2) * H * D;
   a.N = D;
   a.K = 2 * H;
+  if (apply_shared(a, shared, tile_rows, "ffmoe_gemm_dgrad")) return 1;
   return launch_rows<BN, false, EPI_STORE>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
                                            "gemm_dgrad");
+}
+
+extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t* offsets,
+                                const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                                int H, int D, void* ghb_out, void* sk_workspace, void* stream) {
+  return ffmoe_gemm_dgrad_shared(gup, w_up, offsets, tile_offsets, tile_rows, E, max_rows, H, D, ghb_out,
+                                 nullptr, sk_workspace, stream);
 }
 
 // Dense GEMM launch: tiles of BM x BN, the K split S chosen so the grid
@@ -1575,8 +1684,8 @@ int ffmoe::gate_grad_mfma(const void* gl, const void* x, int64_t N, int D, int E
 #endif
 static int wgrad_lpt(int E) { return E >= FFMOE_WGRAD_LPT_MIN_E && E <= kLptMaxE; }
 
-extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
-                                int Nc, void* c_out, void* stream) {
+extern "C" int ffmoe_gemm_wgrad_shared(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
+                                       int Nc, void* c_out, const ffmoe_dense_group* shared, void* stream) {
   if (E < 1 || M <= 0 || M % 8 != 0 || Nc <= 0 || Nc % 8 != 0)
     return set_error("ffmoe_gemm_wgrad: M and Nc must be positive multiples of 8");
   constexpr int BM = 256, BN = 256;
@@ -1596,5 +1705,21 @@ extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* o
   a.n_tiles = (Nc + BN - 1) / BN;
   a.total_tiles = static_cast<int64_t>(E) * a.m_tiles * a.n_tiles;
   a.lpt = wgrad_lpt(E);
+  if (shared != nullptr && shared->rows > 0) {
+    // the dense group is group E: K = its rows of a and b, output c [M, Nc]
+    if (shared->a == nullptr || shared->b == nullptr || shared->c == nullptr || shared->rows > 0x7fffffff)
+      return set_error("ffmoe_gemm_wgrad: bad dense extra group");
+    a.xA = static_cast<const bf16_t*>(shared->a);
+    a.xB = static_cast<const bf16_t*>(shared->b);
+    a.xC = static_cast<bf16_t*>(shared->c);
+    a.x_rows = static_cast<int>(shared->rows);
+    a.total_tiles += static_cast<int64_t>(a.m_tiles) * a.n_tiles;
+    a.lpt = E + 1 <= kLptMaxE;
+  }
   return launch<BM, BN, false, false, 1, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_wgrad");
+}
+
+extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
+                                int Nc, void* c_out, void* stream) {
+  return ffmoe_gemm_wgrad_shared(a_, b_, offsets, E, M, Nc, c_out, nullptr, stream);
 }

@@ -97,7 +97,7 @@ class _FusedMoEFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, x, gate, w_up, w_down, expert_bias, cfg, rcfg):
+    def forward(ctx, x, gate, w_up, w_down, expert_bias, s_gate, s_up, s_down, cfg, rcfg, s_act):
         (top_k, activation, gating, capacity_factor, recompute, mt_user, allow_dropped,
          aux_coeff, z_coeff) = cfg
         pre_softmax, scoring, n_group, topk_group, jitter, advanced = rcfg
@@ -153,9 +153,18 @@ class _FusedMoEFunction(torch.autograd.Function):
             if actual_max > mt:
                 raise RuntimeError(_overflow_message(actual_max, mt))
 
-        out, tw, row_of, xs, up, act, down = ops.experts_forward(
+        # MoELayer's shared expert (s_gate/s_up/s_down, nn.py:22-44) runs as a
+        # dense row group of the routed GEMM launches; its output is added by
+        # the combine (nn.py:156-159)
+        has_sh = s_gate is not None
+        w_gu = w_sd = None
+        if has_sh:
+            w_gu = torch.cat([s_gate.to(dtype), s_up.to(dtype)], 0).contiguous()
+            w_sd = s_down.to(dtype).contiguous()
+        (out, tw, row_of, xs, up, act, down, up_sh, act_sh) = ops.experts_forward(
             xc, wu, wd, topk_idx, topk_w, counts, offsets, tile_offsets, ws, top_k, act_id, mt,
-            capacity_mode, not recompute)
+            capacity_mode, not recompute, shared_w_gu=w_gu, shared_w_down=w_sd,
+            shared_act=int(s_act or 0))
         if not capacity_mode:
             tw = topk_w
 
@@ -163,8 +172,12 @@ class _FusedMoEFunction(torch.autograd.Function):
         ctx.rcfg = (bool(advanced and gating == "softmax"), bool(pre_softmax),
                     float(scoring or 0.0))
         ctx.in_dtypes = (x.dtype, gate.dtype, w_up.dtype, w_down.dtype)
+        ctx.has_sh = has_sh
+        ctx.s_act = int(s_act or 0)
+        ctx.sh_dtypes = (s_gate.dtype, s_up.dtype, s_down.dtype) if has_sh else None
         ctx.save_for_backward(xc, gc, wu, wd, logits, topk_idx, tw, lse, counts, offsets,
-                              tile_offsets, row_of, xs, up, act, down, aux_idx, aux_counts)
+                              tile_offsets, row_of, xs, up, act, down, aux_idx, aux_counts,
+                              w_gu, w_sd, up_sh, act_sh)
         ctx.set_materialize_grads(False)  # unused outputs get no zero-filled gradients
         # the softmax aux loss has a gradient only on the reference's slow
         # routing path, whose weights are differentiable torch ops
@@ -181,7 +194,7 @@ class _FusedMoEFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out, g_aux, g_z, _gc, _gs, _gis):
         (xc, gc, wu, wd, logits, topk_idx, tw, lse, counts, offsets, tile_offsets, row_of, xs,
-         up, act, down, aux_idx, aux_counts) = ctx.saved_tensors
+         up, act, down, aux_idx, aux_counts, w_gu, w_sd, up_sh, act_sh) = ctx.saved_tensors
         top_k, act_id, gate_id, capacity_mode, aux_coeff, z_coeff = ctx.cfg
         aux_through, pre_softmax, scoring = ctx.rcfg
         if grad_out is None:
@@ -191,13 +204,21 @@ class _FusedMoEFunction(torch.autograd.Function):
         gz = g_z if z_coeff > 0.0 else None
         # the sigmoid aux gradient's expert fractions come from the losses
         # block's routing (the un-jittered one under input jitter)
-        dx, dgate, dwu, dwd = ops.experts_backward(
+        dx, dgate, dwu, dwd, dw_gu, dw_sd = ops.experts_backward(
             go, xc, gc, wu, wd, logits, topk_idx, tw, lse,
             counts if aux_counts is None else aux_counts, offsets, tile_offsets, row_of, xs, up,
             act, down, ga, gz, top_k, act_id, gate_id, capacity_mode, aux_coeff, z_coeff,
-            aux_through, aux_idx, aux_counts, pre_softmax, scoring)
+            aux_through, aux_idx, aux_counts, pre_softmax, scoring,
+            shared_w_gu=w_gu if ctx.has_sh else None, shared_w_down=w_sd if ctx.has_sh else None,
+            up_sh=up_sh if ctx.has_sh else None, act_sh=act_sh if ctx.has_sh else None,
+            shared_act=ctx.s_act)
         xd, gd, ud, dd = ctx.in_dtypes
-        return dx.to(xd), dgate.to(gd), dwu.to(ud), dwd.to(dd), None, None, None
+        gs = (None, None, None)
+        if ctx.has_sh:
+            H = w_sd.shape[1]
+            sg, su, sd = ctx.sh_dtypes
+            gs = (dw_gu[:H].to(sg), dw_gu[H:].to(su), dw_sd.to(sd))
+        return (dx.to(xd), dgate.to(gd), dwu.to(ud), dwd.to(dd), None, *gs, None, None, None)
 
 
 def set_ep_group(group, backend="nccl"):
@@ -231,6 +252,7 @@ def fused_moe(
     pre_softmax=False,
     input_jitter=0.0,
     expert_bias=None,
+    _shared=None,
 ):
     """Fused MoE layer forward (differentiable).
 
@@ -244,7 +266,10 @@ def fused_moe(
 
     shared_expert_weights / latent_weights only matter to the reference's
     expert-parallel path and are ignored here, as the reference's
-    single-GPU path ignores them.
+    single-GPU path ignores them.  ``_shared`` (internal, used by MoELayer)
+    is (w_gate [H,D], w_up [H,D], w_down [D,H], activation id): the shared
+    expert then runs inside the same GEMM launches and the returned output
+    is bf16(routed + shared).
     """
     if ep_group is not None:
         raise NotImplementedError("expert parallelism is not part of this single-GPU build")
@@ -272,8 +297,11 @@ def fused_moe(
            float(z_loss_coeff))
     rcfg = (bool(pre_softmax), scoring_factor, n_group if groups else None,
             topk_group if groups else None, jitter, bool(advanced))
+    s_gate = s_up = s_down = s_act = None
+    if _shared is not None:
+        s_gate, s_up, s_down, s_act = _shared
     out, aux, z, counts, stats, istats = _FusedMoEFunction.apply(
-        hidden_states, gate_weight, w_up, w_down, expert_bias, cfg, rcfg)
+        hidden_states, gate_weight, w_up, w_down, expert_bias, s_gate, s_up, s_down, cfg, rcfg, s_act)
 
     losses = {}
     if aux_loss_coeff > 0.0:

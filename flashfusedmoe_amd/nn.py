@@ -146,6 +146,16 @@ class MoELayer(nn.Module):
         leading = x.shape[:-1]
         D = x.shape[-1]
         x_flat = x.reshape(-1, D)
+        se = self.shared_expert
+        if se is not None and se.activation not in _SHARED_ACT:
+            raise ValueError(f"Unknown activation: {se.activation}")
+        # the shared expert runs inside the routed GEMM launches (a dense row
+        # group) when its dimensions suit the direct-to-LDS pipeline; else
+        # as its own dense GEMMs after the routed op
+        fold = se is not None and D % 64 == 0 and self.half_ffn % 64 == 0
+        shared = None
+        if fold:
+            shared = (se.w_gate.weight, se.w_up.weight, se.w_down.weight, _SHARED_ACT[se.activation])
         routed, losses = fused_moe(
             x_flat, self.gate.weight, self.w_up, self.w_down, self.top_k,
             activation=self.activation,
@@ -156,11 +166,9 @@ class MoELayer(nn.Module):
             recompute_activations=self.recompute_activations,
             max_tokens_per_expert=self.max_tokens_per_expert,
             allow_dropped_tokens=self.allow_dropped_tokens,
+            _shared=shared,
         )
-        if self.shared_expert is not None:
-            se = self.shared_expert
-            if se.activation not in _SHARED_ACT:
-                raise ValueError(f"Unknown activation: {se.activation}")
+        if se is not None and not fold:
             routed = routed + _SharedGLU.apply(x_flat, se.w_gate.weight, se.w_up.weight,
                                                se.w_down.weight, _SHARED_ACT[se.activation])
         return routed.reshape(*leading, D), losses

@@ -7,6 +7,7 @@ Fake (meta) implementations make the ops traceable by torch.compile.
 Only bfloat16 CUDA(ROCm) tensors are accepted; there is no other path.
 """
 
+import ctypes
 import os
 from typing import List, Optional
 
@@ -184,7 +185,14 @@ def _route_fake(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, nee
 # experts forward: permute + up GEMM/GLU + down GEMM + combine
 # ---------------------------------------------------------------------------
 
-def _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, save_up, st):
+def _byref(g):
+    return None if g is None else ctypes.byref(g)
+
+
+def _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, save_up, st, shared=None):
+    """Routed up GEMM + GLU and down GEMM.  shared = (x, w_gu, w_sd, act) adds
+    the shared expert as a dense row group of the same launches and returns
+    its (up, act, down) as well."""
     T, D = xs.shape
     E, H2, _ = w_up.shape
     H = H2 // 2
@@ -194,22 +202,36 @@ def _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, save_up, st):
     down = torch.empty(T, D, dtype=_BF16, device=dev)
     tr = L.gemm_tile_rows(T, E)
     ws = L.ptr(L.gemm_workspace(dev, st))
-    L.call("ffmoe_gemm_up_glu", L.ptr(xs), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
-           T, D, H, activation, L.ptr(up), L.ptr(act), ws, st)
-    L.call("ffmoe_gemm_down", L.ptr(act), L.ptr(w_down), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
-           T, H, D, L.ptr(down), ws, st)
-    return up, act, down
+    g_up = g_down = None
+    sh = None
+    if shared is not None:
+        x, w_gu, w_sd, sact = shared
+        N = x.shape[0]
+        sh = (torch.empty(N, H2, dtype=_BF16, device=dev), torch.empty(N, H, dtype=_BF16, device=dev),
+              torch.empty(N, D, dtype=_BF16, device=dev))
+        g_up = L.dense_group(x, w_gu, sh[1], N, sact, c2=sh[0])
+        g_down = L.dense_group(sh[1], w_sd, sh[2], N, 0)
+    L.call("ffmoe_gemm_up_glu_shared", L.ptr(xs), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr,
+           E, T, D, H, activation, L.ptr(up), L.ptr(act), _byref(g_up), ws, st)
+    L.call("ffmoe_gemm_down_shared", L.ptr(act), L.ptr(w_down), L.ptr(offsets), L.ptr(tile_offsets), tr,
+           E, T, H, D, L.ptr(down), _byref(g_down), ws, st)
+    return up, act, down, sh
 
 
 @torch.library.custom_op("ffmoe::experts_forward", mutates_args=())
 def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, topk_w: Tensor,
                     counts: Tensor, offsets: Tensor, tile_offsets: Tensor, ws: Tensor, top_k: int,
                     activation: int, mt: int, capacity_mode: bool,
-                    save_activations: bool) -> List[Tensor]:
+                    save_activations: bool, shared_w_gu: Optional[Tensor] = None,
+                    shared_w_down: Optional[Tensor] = None, shared_act: int = 0) -> List[Tensor]:
     """Returns [out bf16 [N,D], topk_w fp32 [N,k] renormalised under capacity
     dropping (empty without capacity: the weights are topk_w unchanged),
-    row_of int32 [N*k], x_sorted bf16 [N*k,D], up, act, down] where
-    up/act/down are empty when save_activations is False."""
+    row_of int32 [N*k], x_sorted bf16 [N*k,D], up, act, down, up_sh, act_sh]
+    where up/act/down are empty when save_activations is False.  With
+    shared_w_gu [2H,D] (gate rows, then up rows) and shared_w_down [D,H] the
+    shared expert runs as a dense row group of the same GEMM launches and
+    `out` is bf16(routed + shared) (nn.py:156-159); up_sh / act_sh are its
+    pre-activation and activation (empty without it)."""
     _check_bf16_gpu("w_up", w_up)
     _check_bf16_gpu("w_down", w_down)
     N, D = x.shape
@@ -223,22 +245,31 @@ def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, t
     row_of = torch.empty(T, dtype=torch.int32, device=dev)
     L.call("ffmoe_permute", L.ptr(x), L.ptr(topk_idx), L.ptr(tw), L.ptr(offsets), L.ptr(counts),
            N, D, E, k, mt, int(capacity_mode), L.ptr(ws), L.ptr(xs), L.ptr(row_of), st)
-    up, act, down = _up_down(xs, w_up, w_down, offsets, tile_offsets, activation,
-                             save_activations, st)
+    shared = None
+    if shared_w_gu is not None:
+        _check_bf16_gpu("shared expert w_gate|w_up", shared_w_gu)
+        _check_bf16_gpu("shared expert w_down", shared_w_down)
+        shared = (x, shared_w_gu, shared_w_down, shared_act)
+    up, act, down, sh = _up_down(xs, w_up, w_down, offsets, tile_offsets, activation,
+                                 save_activations, st, shared)
     out = torch.empty(N, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_combine", L.ptr(down), L.ptr(row_of), L.ptr(tw), None, N, D, k, L.ptr(out), st)
+    # the shared expert's output is the combine's addend: bf16(bf16(sum) + shared)
+    L.call("ffmoe_combine", L.ptr(down), L.ptr(row_of), L.ptr(tw), None if sh is None else L.ptr(sh[2]),
+           N, D, k, L.ptr(out), st)
     if _CHECK_GEMM:
         L.check_gemm_workspaces()
     tw_out = tw if capacity_mode else topk_w.new_empty(0)
     empty = x.new_empty(0)
+    sh_out = [empty.clone(), empty.clone()] if sh is None else [sh[0], sh[1]]
     if not save_activations:
-        return [out, tw_out, row_of, xs, empty, empty.clone(), empty.clone()]
-    return [out, tw_out, row_of, xs, up, act, down]
+        return [out, tw_out, row_of, xs, empty, empty.clone(), empty.clone(), *sh_out]
+    return [out, tw_out, row_of, xs, up, act, down, *sh_out]
 
 
 @experts_forward.register_fake
 def _experts_forward_fake(x, w_up, w_down, topk_idx, topk_w, counts, offsets, tile_offsets, ws,
-                          top_k, activation, mt, capacity_mode, save_activations):
+                          top_k, activation, mt, capacity_mode, save_activations, shared_w_gu=None,
+                          shared_w_down=None, shared_act=0):
     N, D = x.shape
     H2 = w_up.shape[1]
     T = N * top_k
@@ -247,8 +278,9 @@ def _experts_forward_fake(x, w_up, w_down, topk_idx, topk_w, counts, offsets, ti
         acts = [e(T, H2), e(T, H2 // 2), e(T, D)]
     else:
         acts = [e(0), e(0), e(0)]
+    sh = [e(N, H2), e(N, H2 // 2)] if shared_w_gu is not None else [e(0), e(0)]
     tw = topk_w.new_empty(topk_w.shape) if capacity_mode else topk_w.new_empty(0)
-    return [e(N, D), tw, e(T, dtype=torch.int32), e(T, D), *acts]
+    return [e(N, D), tw, e(T, dtype=torch.int32), e(T, D), *acts, *sh]
 
 
 # ---------------------------------------------------------------------------
@@ -263,11 +295,18 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
                      top_k: int, activation: int, gating: int, capacity_mode: bool,
                      aux_coeff: float, z_coeff: float, aux_through_weights: bool = False,
                      aux_idx: Optional[Tensor] = None, aux_counts: Optional[Tensor] = None,
-                     pre_softmax: bool = False, scoring: float = 0.0) -> List[Tensor]:
+                     pre_softmax: bool = False, scoring: float = 0.0,
+                     shared_w_gu: Optional[Tensor] = None, shared_w_down: Optional[Tensor] = None,
+                     up_sh: Optional[Tensor] = None, act_sh: Optional[Tensor] = None,
+                     shared_act: int = 0) -> List[Tensor]:
     """Returns [grad_hidden [N,D], grad_gate [E,D], grad_w_up [E,2H,D],
-    grad_w_down [E,D,H]], all bf16.  Empty up/act/down trigger recompute.
-    logits / lse are the un-jittered ones; aux_* describe the aux loss's own
-    routing (ffmoe_route_bwd_ex)."""
+    grad_w_down [E,D,H], grad_shared_w_gu [2H,D], grad_shared_w_down [D,H]],
+    all bf16 (the last two empty without the shared expert).  Empty
+    up/act/down trigger recompute.  logits / lse are the un-jittered ones;
+    aux_* describe the aux loss's own routing (ffmoe_route_bwd_ex).  With the
+    shared expert (its weights and saved up_sh / act_sh) its four GEMMs run as
+    a dense row group of the routed launches, and grad_hidden includes its
+    input gradient."""
     _check_bf16_gpu("grad_output", go)
     N, D = x.shape
     E, H2, _ = w_up.shape
@@ -277,7 +316,20 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     dev = x.device
     st = L.stream_ptr(dev)
     if up.numel() == 0:  # recompute_activations: same kernels, same bits
-        up, act, down = _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, True, st)
+        up, act, down, _ = _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, True, st)
+    has_sh = shared_w_gu is not None
+    g_wd = g_dg = g_wu = g_dx = None
+    if has_sh:
+        dw_gu_sh = torch.empty(H2, D, dtype=_BF16, device=dev)
+        dw_sd_sh = torch.empty(D, H, dtype=_BF16, device=dev)
+        gup_sh = torch.empty(N, H2, dtype=_BF16, device=dev)
+        dx_sh = torch.empty(N, D, dtype=_BF16, device=dev)
+        # the shared expert's grads (nn.py:22-44 under autograd): its output
+        # gradient is go itself
+        g_wd = L.dense_group(go, act_sh, dw_sd_sh, N, 0)           # go^T act
+        g_dg = L.dense_group(go, shared_w_down, gup_sh, N, shared_act, up=up_sh)  # GLU'(go w_down)
+        g_wu = L.dense_group(gup_sh, x, dw_gu_sh, N, 0)            # gup^T x
+        g_dx = L.dense_group(gup_sh, shared_w_gu, dx_sh, N, 0)     # gup w_gu
     wgo = torch.empty(T, D, dtype=_BF16, device=dev)
     gl = torch.empty(N, E, dtype=_BF16, device=dev)
     ga = None if g_aux is None else g_aux.to(device=dev, dtype=torch.float32).contiguous()
@@ -291,20 +343,22 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     # routing backward just wrote are cache-resident (measured 0.5% faster per
     # C2 step than after the dX GEMMs)
     dwd = torch.empty(E, D, H, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_wgrad", L.ptr(wgo), L.ptr(act), L.ptr(offsets), E, D, H, L.ptr(dwd), st)
+    L.call("ffmoe_gemm_wgrad_shared", L.ptr(wgo), L.ptr(act), L.ptr(offsets), E, D, H, L.ptr(dwd),
+           _byref(g_wd), st)
     gup = torch.empty(T, H2, dtype=_BF16, device=dev)
     tr = L.gemm_tile_rows(T, E)
     ws = L.ptr(L.gemm_workspace(dev, st))
-    L.call("ffmoe_gemm_dgrad_glu", L.ptr(wgo), L.ptr(w_down), L.ptr(up), L.ptr(offsets),
-           L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(gup), ws, st)
+    L.call("ffmoe_gemm_dgrad_glu_shared", L.ptr(wgo), L.ptr(w_down), L.ptr(up), L.ptr(offsets),
+           L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(gup), _byref(g_dg), ws, st)
     # the up-projection weight gradient right after the GEMM that wrote `gup`
     # (128 MiB at C2) while it is still cache-resident; measured ~1% faster
     # per step than after the dX GEMMs
     dwu = torch.empty(E, H2, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_wgrad", L.ptr(gup), L.ptr(xs), L.ptr(offsets), E, H2, D, L.ptr(dwu), st)
+    L.call("ffmoe_gemm_wgrad_shared", L.ptr(gup), L.ptr(xs), L.ptr(offsets), E, H2, D, L.ptr(dwu),
+           _byref(g_wu), st)
     ghb = torch.empty(T, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_dgrad", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr, E,
-           T, H, D, L.ptr(ghb), ws, st)
+    L.call("ffmoe_gemm_dgrad_shared", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr,
+           E, T, H, D, L.ptr(ghb), _byref(g_dx), ws, st)
     dx = torch.empty(N, D, dtype=_BF16, device=dev)
     fused_gate = E <= L.MAX_FUSED_GATE_E
     if fused_gate:  # the gl @ gate term is computed inside the dX reduce
@@ -317,13 +371,24 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     dgate = gate_grad(gl, x)
     if _CHECK_GEMM:
         L.check_gemm_workspaces()
-    return [dx, dgate, dwu, dwd]
+    if not has_sh:
+        e0 = x.new_empty(0)
+        return [dx, dgate, dwu, dwd, e0, e0.clone()]
+    # x's gradient from both branches, bf16 + bf16 as autograd accumulates it
+    return [dx + dx_sh, dgate, dwu, dwd, dw_gu_sh, dw_sd_sh]
 
 
 @experts_backward.register_fake
-def _experts_backward_fake(go, x, gate, w_up, w_down, *rest):
+def _experts_backward_fake(go, x, gate, w_up, w_down, logits, topk_idx, topk_w, lse, counts, offsets,
+                           tile_offsets, row_of, xs, up, act, down, g_aux, g_z, top_k, activation,
+                           gating, capacity_mode, aux_coeff, z_coeff, aux_through_weights=False,
+                           aux_idx=None, aux_counts=None, pre_softmax=False, scoring=0.0,
+                           shared_w_gu=None, shared_w_down=None, up_sh=None, act_sh=None,
+                           shared_act=0):
+    sh = ([shared_w_gu.new_empty(shared_w_gu.shape), shared_w_down.new_empty(shared_w_down.shape)]
+          if shared_w_gu is not None else [x.new_empty(0), x.new_empty(0)])
     return [x.new_empty(x.shape), gate.new_empty(gate.shape), w_up.new_empty(w_up.shape),
-            w_down.new_empty(w_down.shape)]
+            w_down.new_empty(w_down.shape), *sh]
 
 
 # ---------------------------------------------------------------------------

@@ -180,6 +180,49 @@ int ffmoe_gemm_tile_rows(int64_t max_rows, int E);
  * No reference counterpart (the reference's GEMMs are cuBLAS bmm calls). */
 int64_t ffmoe_gemm_workspace_bytes(void);
 
+/* A dense row group computed in the same launch as the routed experts (the
+ * shared expert of MoELayer, nn.py:22-44, :156-159): its row tiles follow
+ * the routed tiles of each *_shared GEMM below, with the same K and N as one
+ * routed expert.  For the grouped-rows GEMMs `a` holds its A rows
+ * [rows, K], `b` its weight matrix (laid out as one routed expert's), `c`
+ * its output rows, `c2` (GLU forward, may be NULL) its pre-activation
+ * output, `up` (GLU backward) its pre-activation input; for
+ * ffmoe_gemm_wgrad_shared it is group E, K = its rows: c [M, Nc] =
+ * a[rows, M]^T · b[rows, Nc].  `activation` is its GLU (FFMOE_ACT_*). */
+typedef struct ffmoe_dense_group {
+  const void* a;
+  const void* b;
+  const void* up;
+  void* c;
+  void* c2;
+  int64_t rows;
+  int activation;
+} ffmoe_dense_group;
+
+/* The grouped-rows GEMMs with a dense extra group in the same launch
+ * (shared may be NULL: then identical to the plain entry points).  No
+ * reference counterpart (the reference runs the shared expert as three
+ * nn.Linear modules outside the fused op). */
+int ffmoe_gemm_up_glu_shared(const void* x_sorted, const void* w_up, const int32_t* offsets,
+                             const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                             int D, int H, int activation, void* up_out, void* act_out,
+                             const ffmoe_dense_group* shared, void* sk_workspace, void* stream);
+int ffmoe_gemm_down_shared(const void* act, const void* w_down, const int32_t* offsets,
+                           const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                           int H, int D, void* down_out, const ffmoe_dense_group* shared,
+                           void* sk_workspace, void* stream);
+int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, const void* up,
+                                const int32_t* offsets, const int32_t* tile_offsets,
+                                int tile_rows, int E, int64_t max_rows, int D, int H,
+                                int activation, void* gup_out, const ffmoe_dense_group* shared,
+                                void* sk_workspace, void* stream);
+int ffmoe_gemm_dgrad_shared(const void* gup, const void* w_up, const int32_t* offsets,
+                            const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                            int H, int D, void* ghb_out, const ffmoe_dense_group* shared,
+                            void* sk_workspace, void* stream);
+int ffmoe_gemm_wgrad_shared(const void* a, const void* b, const int32_t* offsets, int E, int M,
+                            int Nc, void* c_out, const ffmoe_dense_group* shared, void* stream);
+
 /* Reports a failed stream-K partner wait of an earlier grouped GEMM on
  * sk_workspace.  The wait is bounded; it is not expected to time out (the
  * block it waits for is already running), but if it does the GEMM's output

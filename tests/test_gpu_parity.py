@@ -96,7 +96,7 @@ def test_permutation_bit_exact(N, E, k, mt, cap):
     xg, gg, wug, wdg = cuda(x, gate, wu, wd)
     (logits, idx, tw, lse, counts, offsets, tile_off, stats, istats, ws, _aux, _z) = ops.route(
         xg, gg, None, k, 0, mt, 0.0, 0.0, False)
-    out, tw2, row_of, xs, up, act, down = ops.experts_forward(
+    out, tw2, row_of, xs, up, act, down, _, _ = ops.experts_forward(
         xg, wug, wdg, idx, tw, counts, offsets, tile_off, ws, k, 0, mt, cap, True)
     exp_rows, exp_counts, exp_off = expected_rows(idx.cpu().numpy(), E, mt, cap)
     assert np.array_equal(counts.cpu().numpy(), exp_counts)

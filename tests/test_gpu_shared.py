@@ -63,11 +63,16 @@ def test_dense_glu_against_fp32(act, N, D, H):
 
 
 @pytest.mark.parametrize("act", ACTS)
-def test_moelayer_shared_expert_forward_backward(act):
+@pytest.mark.parametrize("D,ffn,fold", [(128, 256, True), (136, 208, False)])
+def test_moelayer_shared_expert_forward_backward(act, D, ffn, fold):
+    """fold: D and ffn/2 multiples of 64, the shared expert runs as a dense
+    row group of the routed GEMM launches; otherwise as its own dense GEMMs
+    (ffmoe_glu_fwd / ffmoe_glu_bwd between them)."""
     from flashfusedmoe_amd import MoELayer
+    from flashfusedmoe_amd import _lib as L
     from flashfusedmoe_amd import ops
     torch.manual_seed(3)
-    D, ffn, E, k, N = 128, 256, 8, 2, 512
+    E, k, N = 8, 2, 512
     layer = MoELayer(D, ffn, E, top_k=k, activation=act, num_shared_experts=1)
     layer = layer.to(torch.bfloat16)
     ref_shared = layer.shared_expert  # CPU copy of the parameters (reference formula)
@@ -77,9 +82,16 @@ def test_moelayer_shared_expert_forward_backward(act):
     x = torch.randn(2, N // 2, D, generator=g).to(torch.bfloat16)
     go = torch.randn(2, N // 2, D, generator=g).to(torch.bfloat16)
     xg = x.cuda().requires_grad_(True)
-    out, _ = layer(xg)
-    out.backward(go.cuda())
-    torch.cuda.synchronize()
+    called = []
+    L.call_hook = lambda name, phase: called.append(name) if phase == 0 else None
+    try:
+        out, _ = layer(xg)
+        out.backward(go.cuda())
+        torch.cuda.synchronize()
+    finally:
+        L.call_hook = None
+    assert ("ffmoe_glu_fwd" in called) == (not fold)
+    assert ("ffmoe_glu_bwd" in called) == (not fold)
 
     # routed part: the oracle on the GPU's own gate logits
     xf = x.reshape(N, D)
