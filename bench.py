@@ -26,8 +26,10 @@ Prints ONE JSON line.  Besides the contract fields it carries:
 
 ``--traffic`` runs each hot kernel twice, after a 256 MiB calibration copy
 and with a 1 GiB flush before every launch, and prints nothing else: the
-driver of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes whose summary
-is profiles/hbm_traffic_c2.md.
+driver of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes.
+``--traffic-summary FETCH_CSV WRITE_CSV`` (no GPU) turns the two passes'
+counter CSVs into profiles/hbm_traffic_c2.md, which bench.py reads back for
+the `traffic` fields.
 """
 
 import argparse
@@ -324,25 +326,195 @@ def cpu_baseline(c, sample_tokens, runs=7):
                        f"{sum(times):.1f} s timed)")
 
 
+# the order traffic_mode launches the hot kernels in (each twice, after a flush)
+TRAFFIC_ORDER = ["gemm_up_glu", "gemm_down", "gemm_dgrad_glu", "gemm_dgrad", "gemm_wgrad_down",
+                 "gemm_wgrad_up", "route_fwd", "permute", "combine", "route_bwd", "dx_reduce",
+                 "gate_grad"]
+CAL_KIB = 256 * 1024  # the calibration copy reads and writes 256 MiB
+
+
 def traffic_mode(c, x, gate, wu, wd, go):
     """Each hot kernel twice, after a 256 MiB calibration copy, with a 1 GiB
     flush before every launch (the rocprofv3 --pmc driver)."""
     fns, _, keep = kernel_launches(c, x, gate, wu, wd, go)
+    assert sorted(fns) == sorted(TRAFFIC_ORDER)
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=x.device)
-    src = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=x.device).uniform_()
+    src = torch.empty(CAL_KIB * 256, dtype=torch.float32, device=x.device).uniform_()
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written
+    torch.mul(src, 1.0, out=dst)  # calibration: a plain elementwise copy kernel
     torch.cuda.synchronize()
     del src, dst
-    for name, fn in fns.items():
+    for name in TRAFFIC_ORDER:
         for _ in range(2):
             flush.zero_()
-            fn()
+            fns[name]()
         torch.cuda.synchronize()
         print(f"traffic: {name} launched twice", flush=True)
     del keep
     print("traffic done", flush=True)
+
+
+def read_pmc_csv(path):
+    """[(dispatch id, kernel name, value)] in dispatch order from a rocprofv3
+    --pmc counter_collection.csv holding one counter."""
+    import csv
+    acc = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            d = int(r["Dispatch_Id"])
+            name, v = acc.get(d, (r["Kernel_Name"], 0.0))
+            acc[d] = (name, v + float(r["Counter_Value"]))
+    return [(d, *acc[d]) for d in sorted(acc)]
+
+
+def traffic_per_kernel(rows):
+    """Splits traffic_mode's dispatches (the tail of the run): the last
+    2*len(TRAFFIC_ORDER) flush fills each open one launch of the next kernel
+    in TRAFFIC_ORDER; the dispatch before the first of them is the
+    calibration copy.  Returns ({kernel: mean counter over its 2 launches},
+    calibration counter, calibration kernel name)."""
+    fills = [i for i, r in enumerate(rows) if "FillFunctor" in r[1]]
+    n = 2 * len(TRAFFIC_ORDER)
+    if len(fills) < n:
+        raise ValueError(f"expected at least {n} flush fills, found {len(fills)}")
+    loop = fills[-n:]
+    cal = rows[loop[0] - 1]
+    if "FillFunctor" in cal[1] or "Mul" not in cal[1]:
+        raise ValueError(f"the dispatch before the first flush is not the calibration copy: {cal[1]}")
+    bounds = loop + [len(rows)]
+    per = {}
+    for j, name in enumerate(TRAFFIC_ORDER):
+        vals = []
+        for l in (2 * j, 2 * j + 1):
+            seg = rows[bounds[l] + 1:bounds[l + 1]]
+            if not seg:
+                raise ValueError(f"no dispatch after flush {l} ({name})")
+            vals.append(sum(r[2] for r in seg))
+        per[name] = sum(vals) / 2
+    return per, cal[2], cal[1]
+
+
+def algorithmic_bytes(c, rows):
+    """Operand + output bytes of one launch of each grouped GEMM (every
+    operand read once, every output written once) and the bandwidth
+    kernels' algorithmic bytes."""
+    N, D, E = c["N"], c["D"], c["E"]
+    H = c["ffn"] // 2
+    b = 2
+    out = {
+        "gemm_up_glu": rows * D * b + E * 2 * H * D * b + rows * 2 * H * b + rows * H * b,
+        "gemm_down": rows * H * b + E * D * H * b + rows * D * b,
+        "gemm_dgrad_glu": rows * D * b + E * D * H * b + 2 * rows * 2 * H * b,
+        "gemm_dgrad": rows * 2 * H * b + E * 2 * H * D * b + rows * D * b,
+        "gemm_wgrad_down": rows * D * b + rows * H * b + E * D * H * b,
+        "gemm_wgrad_up": rows * 2 * H * b + rows * D * b + E * 2 * H * D * b,
+    }
+    for name, (w, kind) in algorithmic_work(c, rows).items():
+        if kind == "byte" and w is not None:
+            out[name] = int(w)
+    return out
+
+
+def traffic_summary(fetch_csv, write_csv, out_path, commands):
+    """Writes the FETCH_SIZE / WRITE_SIZE summary (markdown, with the
+    machine-readable traffic_bytes lines measured_traffic reads)."""
+    fetch, cal_f, cal_name = traffic_per_kernel(read_pmc_csv(fetch_csv))
+    write, cal_w, _ = traffic_per_kernel(read_pmc_csv(write_csv))
+    sf, sw = CAL_KIB / cal_f, CAL_KIB / cal_w
+    c = CFG
+    alg = algorithmic_bytes(c, c["N"] * c["k"])
+    lines = [
+        "# HBM traffic per launch of the hot kernels (C2: N8192 D1024 ffn4096 E8 k2, all rows routed)",
+        "",
+        "Commands (from the repository root on one MI355X; two passes, one counter each; then the",
+        "summary is written from the two counter_collection.csv files):",
+        "",
+        "```",
+        *commands,
+        "```",
+        "",
+        f"Calibration: `{cal_name[:90]}` copies 256 MiB (reads 262144 KiB, writes 262144 KiB).",
+        f"FETCH_SIZE reads {cal_f:.0f} KiB for it (scale x{sf:.3f}), WRITE_SIZE {cal_w:.0f} KiB "
+        f"(scale x{sw:.3f}).",
+        "Every kernel runs twice, each launch after a 1 GiB write that evicts the L2s and the MALL;",
+        "the table averages the two launches.  FETCH_SIZE counts the L2's requests to the memory",
+        "fabric, so a MALL hit inside one launch still counts as traffic.",
+        "",
+        "| Kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) | algorithmic bytes | ratio |",
+        "|---|---:|---:|---:|---:|---:|",
+    ]
+    mach = []
+    for name in TRAFFIC_ORDER:
+        tb = int(round((fetch[name] * sf + write[name] * sw) * 1024))
+        a = alg.get(name)
+        ratio = f"{tb / a:.2f}" if a else "-"
+        lines.append(f"| {name} | {fetch[name]:.0f} | {write[name]:.0f} | {tb} | {a if a else '-'} | {ratio} |")
+        mach.append(f"traffic_bytes {name} {tb}")
+    lines += ["", "Machine-readable (read by bench.py for `traffic`):", "", "```", *mach, "```", ""]
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines))
+
+
+# the grouped-GEMM dispatches of one fwd+bwd step, in launch order
+GEMM_STEP_ORDER = ["gemm_up_glu", "gemm_down", "gemm_wgrad_down", "gemm_dgrad_glu", "gemm_wgrad_up",
+                   "gemm_dgrad"]
+
+
+def stats_summary(prof_dir, bench_log, out_path, title, command):
+    """Writes a markdown summary of a rocprofv3 --kernel-trace --stats run of
+    bench.py: the kernel table, which kernel symbol runs each GEMM of the
+    step (read from the trace: the step's first GEMM dispatches in launch
+    order), and the dominant GEMM's rocprof average next to bench.py's
+    in-step HIP-event average."""
+    import csv
+    import glob
+    stats_csv = glob.glob(os.path.join(prof_dir, "*kernel_stats.csv"))[0]
+    trace_csv = glob.glob(os.path.join(prof_dir, "*kernel_trace.csv"))[0]
+    with open(stats_csv, newline="") as f:
+        stats = list(csv.DictReader(f))
+    with open(trace_csv, newline="") as f:
+        trace = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    line = None
+    for ln in open(bench_log):
+        if ln.startswith("{"):
+            line = json.loads(ln)
+    gemm = [r["Kernel_Name"] for r in trace if "ffmoe::gemm_" in r["Kernel_Name"]]
+    role_sym = dict(zip(GEMM_STEP_ORDER, gemm[:len(GEMM_STEP_ORDER)]))
+    total = sum(float(r["TotalDurationNs"]) for r in stats)
+    out = [f"# rocprofv3 kernel statistics: {title}", "",
+           "Command (from the repository root on one MI355X):", "", "```", command, "```", "",
+           f"Total kernel time: {total / 1e6:.3f} ms over the whole run.", "",
+           "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | % of kernel time |",
+           "|---|---:|---:|---:|---:|---:|"]
+    for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"]))[:28]:
+        out.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                   f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                   f"{float(r['Percentage']):.2f} |")
+    out += ["", "Kernel symbol of each grouped GEMM of the step (the first step's GEMM dispatches):", ""]
+    for role in GEMM_STEP_ORDER:
+        sym = role_sym.get(role, "?")
+        durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace
+                if r["Kernel_Name"] == sym]
+        shared = [k for k, v in role_sym.items() if v == sym and k != role]
+        note = f" (same symbol as {', '.join(shared)})" if shared else ""
+        avg = sum(durs) / len(durs) if durs else float("nan")
+        out.append(f"* {role}: `{sym[:100]}`, {len(durs)} launches, avg {avg:.2f} us{note}")
+    if line is not None and line.get("roofline"):
+        rf = line["roofline"]
+        dom = rf["kernel"]
+        sym = role_sym.get(dom)
+        st = next((r for r in stats if r["Name"] == sym), None)
+        out += ["", f"Dominant kernel (`roofline` of the bench line printed by this run): `{dom}`.",
+                f"bench.py's in-step HIP events: {rf['avg_launch_ms'] * 1e3:.2f} us per launch "
+                f"({rf['achieved']} TFLOP/s, {rf['frac'] * 100:.1f}% of the bf16 MFMA peak)."]
+        if st is not None:
+            out.append(f"rocprofv3's average over the {st['Calls']} launches of its symbol in this run: "
+                       f"{float(st['AverageNs']) / 1e3:.2f} us.")
+        out.append(f"Step time of this run: {line['ms_per_step']} ms ({line['value']} tokens/s).")
+    out.append("")
+    with open(out_path, "w") as f:
+        f.write("\n".join(out))
 
 
 def main():
@@ -356,7 +528,23 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the MoELayer (shared expert) timing")
     ap.add_argument("--instr-steps", type=int, default=10, help="instrumented steps for in-step kernel times")
     ap.add_argument("--traffic", action="store_true", help="rocprofv3 --pmc driver mode")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write the traffic summary from the two --pmc passes' counter CSVs (no GPU)")
+    ap.add_argument("--stats-summary", nargs=5, metavar=("PROF_DIR", "BENCH_LOG", "OUT_MD", "TITLE", "COMMAND"),
+                    help="write a kernel-statistics summary of a rocprofv3 run of bench.py (no GPU)")
     args = ap.parse_args()
+    if args.stats_summary:
+        stats_summary(*args.stats_summary)
+        return
+    if args.traffic_summary:
+        fcsv, wcsv = args.traffic_summary
+        cmds = [f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 90 rocprofv3 --pmc {ctr} "
+                f"--output-format csv -d $REPO/gpurun_out/pmc_{tag} -o p -- python3 $REPO/bench.py --traffic"
+                for ctr, tag in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write"))]
+        cmds.append("python3 bench.py --traffic-summary gpurun_out/pmc_fetch/p_counter_collection.csv "
+                    "gpurun_out/pmc_write/p_counter_collection.csv")
+        traffic_summary(fcsv, wcsv, TRAFFIC_FILE, cmds)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)

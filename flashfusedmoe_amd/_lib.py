@@ -52,7 +52,7 @@ SIGNATURES = {
     "ffmoe_gemm_down_shared": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P, _P]),
     "ffmoe_gemm_dgrad_glu_shared": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P, _P]),
     "ffmoe_gemm_dgrad_shared": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P, _P]),
-    "ffmoe_gemm_wgrad_shared": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _P]),
+    "ffmoe_gemm_wgrad_shared": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _P, _P]),
     "ffmoe_combine": (_I, [_P, _P, _P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_dx_reduce": (_I, [_P, _P, _P, _P, _L, _I, _I, _I, _P, _P]),
     "ffmoe_gate_grad_workspace_bytes": (_L, [_L, _I, _I]),

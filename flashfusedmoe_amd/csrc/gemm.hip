@@ -58,6 +58,8 @@ struct GemmArgs {
   int act;
   float* part;  // persistent kernel: fp32 partial tiles, one slot per block
   int* flags;   // persistent kernel: one flag per block + an error word
+  int pub_off;  // cut tiles: publication of counter `key` is flags[pub_off + key]
+  int err_idx;  // cut tiles: the error word is flags[err_idx]
   int lpt;      // wgrad: test the routing skew and balance the tiles over the XCDs
   int64_t split_rows;  // split-K: rows of one fp32 partial slab
   // An optional dense row group after the routed experts (the shared expert
@@ -71,7 +73,24 @@ struct GemmArgs {
   const bf16_t* xUp;
   int x_rows;
   int x_act;
+  // grouped K only: x_split = 2 cuts the dense group's K into two groups of
+  // x_chunk and x_rows - x_chunk rows whose tiles are finished as cut tiles
+  // (counter flags[kPairKey + tile], fp32 partial in slot `tile`)
+  int x_split;
+  int x_chunk;
 };
+
+// Grouped K: groups of the extra dense group (two when its K is split).
+__device__ __forceinline__ int extra_groups(const GemmArgs& p) {
+  return p.x_rows > 0 ? (p.x_split > 1 ? 2 : 1) : 0;
+}
+
+// Grouped K: rows (K) of group i (the routed experts, then the dense group's).
+__device__ __forceinline__ int group_rows(const GemmArgs& p, int i) {
+  if (i < p.E) return p.offsets[i + 1] - p.offsets[i];
+  if (p.x_split < 2) return p.x_rows;
+  return i == p.E ? p.x_chunk : p.x_rows - p.x_chunk;
+}
 
 // Row tiles of the extra dense group.
 template <int BM>
@@ -602,6 +621,7 @@ struct TileCoord {
   int e, m0, n0, row_begin, row_end;
   bool valid;
   bool extra;  // a tile of the extra dense group
+  int xt;      // grouped K, extra group: the tile's index in its group
 };
 
 // Row-group tables are read through the constant address space: they do not
@@ -651,11 +671,13 @@ __device__ __forceinline__ TileCoord decode_k_tile(const GemmArgs& p, int64_t t)
   c.m0 = mt * BM;
   c.n0 = nt * BN;
   c.valid = true;
-  if (c.e >= p.E) {  // the extra dense group: all of its rows
+  if (c.e >= p.E) {  // the extra dense group: all of its rows, or one of two K halves
+    const int half = c.e - p.E;
     c.extra = true;
+    c.xt = static_cast<int>(t - static_cast<int64_t>(c.e) * per_e);
     c.e = 0;
-    c.row_begin = 0;
-    c.row_end = p.x_rows;
+    c.row_begin = half == 0 ? 0 : p.x_chunk;
+    c.row_end = (half == 0 && p.x_split > 1) ? p.x_chunk : p.x_rows;
     return c;
   }
   c.row_begin = ld_const(p.offsets, c.e);
@@ -988,25 +1010,25 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       wait_vmcnt_le(0);
       __syncthreads();
       if (tid == 0)
-        __hip_atomic_store(p.flags + gridDim.x + key, slot + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.flags + p.pub_off + key, slot + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
     // second arrival: wait for the publication (bounded: its writer is past
     // the counter, i.e. running), then clear both words for the next launch
     if (tid == 0) {
       int src = 0, polls = 0;
-      while ((src = __hip_atomic_load(p.flags + gridDim.x + key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0 &&
+      while ((src = __hip_atomic_load(p.flags + p.pub_off + key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0 &&
              ++polls < kSpinLimit)
         __builtin_amdgcn_s_sleep(8);
       if (src != 0) {
         __hip_atomic_store(p.flags + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.flags + gridDim.x + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.flags + p.pub_off + key, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else {
         // Never expected.  The tile is finished without the partner's
         // partial and the error word is set; both flag words are left as
         // they are (the partner may still publish), so the workspace stays
         // unusable until ffmoe_gemm_check() reports the error and clears it.
-        __hip_atomic_store(p.flags + 2 * gridDim.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.flags + p.err_idx, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       *s_word = src - 1;  // -1: no partial to add
     }
@@ -1072,6 +1094,13 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
 }
 
 constexpr int kLptMaxE = 1024;  // experts the skew-balanced wgrad order handles
+// Flag words of the split dense-group wgrad tiles in the persistent GEMMs'
+// workspace: counters [kPairKey, kPairKey + kPairMax), publications
+// kPairPubOff words further on.  The persistent GEMMs' own words take
+// [0, 2G] (G = CUs), so this needs 2G < kPairKey.
+constexpr int kPairKey = 1024;
+constexpr int kPairPubOff = 512;
+constexpr int kPairMax = 512;
 
 // One block per tile.
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
@@ -1105,17 +1134,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
       // same decision (one ballot), so the test needs no block barrier.
       // Loads go out four per lane at a time (clamped in range) before any
       // is waited for.
-      // the extra dense group (if any) is group E, with x_rows rows
-      const int NG = p.E + (p.x_rows > 0 ? 1 : 0);
+      // the extra dense group (if any) is group E (and E + 1: its second K half)
+      const int NG = p.E + extra_groups(p);
       const int64_t total3 = 3 * (static_cast<int64_t>(p.offsets[p.E] - p.offsets[0]) + (p.x_rows > 0 ? p.x_rows : 0));
       bool heavy = false;
       for (int i0 = threadIdx.x & 63; i0 < NG; i0 += 256) {
         int cnt[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i = min(i0 + 64 * u, NG - 1);
-          cnt[u] = i < p.E ? p.offsets[min(i, p.E - 1) + 1] - p.offsets[min(i, p.E - 1)] : p.x_rows;
-        }
+        for (int u = 0; u < 4; ++u) cnt[u] = group_rows(p, min(i0 + 64 * u, NG - 1));
 #pragma unroll
         for (int u = 0; u < 4; ++u)
           heavy |= i0 + 64 * u < NG && 2 * static_cast<int64_t>(cnt[u]) * NG >= total3;
@@ -1127,17 +1153,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
       // group, and the groups are visited heaviest first (ties: lower
       // index first), so the long tiles start at once and the short ones
       // fill in behind them.
-      __shared__ int s_cnt[kLptMaxE + 1];
+      __shared__ int s_cnt[kLptMaxE + 2];
       __shared__ int s_sel;
-      const int NG = p.E + (p.x_rows > 0 ? 1 : 0);
+      const int NG = p.E + extra_groups(p);
       const int per_e = p.m_tiles * p.n_tiles;
       const int c = (per_e + 7) / 8;
       const int sl = static_cast<int>(blockIdx.x >> 3);
       const int r = sl / c;                                           // rank of the group
       const int sub = static_cast<int>(blockIdx.x & 7) * c + sl % c;  // its tile
       if (r >= NG || sub >= per_e) return;
-      for (int i = threadIdx.x; i < NG; i += kThreads)
-        s_cnt[i] = i < p.E ? p.offsets[i + 1] - p.offsets[i] : p.x_rows;
+      for (int i = threadIdx.x; i < NG; i += kThreads) s_cnt[i] = group_rows(p, i);
       __syncthreads();
       for (int i = threadIdx.x; i < NG; i += kThreads) {
         const int ci = s_cnt[i];
@@ -1156,7 +1181,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
   }
   if (!tc.valid) return;
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
-  gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
+  if (MODE == 1 && tc.extra && p.x_split > 1)  // one K half of a split dense-group tile
+    gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_CUT, tc.xt, kPairKey + tc.xt);
+  else
+    gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
 #endif
 }
 
@@ -1292,7 +1320,7 @@ static int launch(const GemmArgs& a, hipStream_t st, const char* name) {
   const bool dl = g_use_tr && (MODE == 1 || a.K % DL_BK == 0);
   if (a.x_rows > 0 && !dl)
     return set_error(std::string(name) + ": a dense extra group needs K a multiple of 64 and the transpose-read path");
-  const int groups = a.E + (a.x_rows > 0 ? 1 : 0);
+  const int groups = a.E + (a.x_rows > 0 ? (a.x_split > 1 ? 2 : 1) : 0);
   const int64_t grid = (dl && a.lpt) ? static_cast<int64_t>(groups) * 8 * ((a.m_tiles * a.n_tiles + 7) / 8)
                                      : (a.total_tiles + 7) / 8 * 8;
   if (grid > 0x7fffffff) return set_error(std::string(name) + ": problem too large");
@@ -1340,6 +1368,8 @@ static int launch_sk(GemmArgs a, void* ws, int min_k, hipStream_t st, const char
   if (G <= 0) return set_error(std::string(name) + ": cannot query the CU count");
   a.flags = static_cast<int*>(ws);
   a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kSkFlagBytes);
+  a.pub_off = G;
+  a.err_idx = 2 * G;
   hipLaunchKernelGGL((gemm_sk_kernel<BM, BN, true, B_KC, EPI>), dim3(G), dim3(kThreads), 0, st, a);
   if (check_launch(name)) return 1;
   return clear_error();
@@ -1685,7 +1715,8 @@ int ffmoe::gate_grad_mfma(const void* gl, const void* x, int64_t N, int D, int E
 static int wgrad_lpt(int E) { return E >= FFMOE_WGRAD_LPT_MIN_E && E <= kLptMaxE; }
 
 extern "C" int ffmoe_gemm_wgrad_shared(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
-                                       int Nc, void* c_out, const ffmoe_dense_group* shared, void* stream) {
+                                       int Nc, void* c_out, const ffmoe_dense_group* shared, void* sk_workspace,
+                                       void* stream) {
   if (E < 1 || M <= 0 || M % 8 != 0 || Nc <= 0 || Nc % 8 != 0)
     return set_error("ffmoe_gemm_wgrad: M and Nc must be positive multiples of 8");
   constexpr int BM = 256, BN = 256;
@@ -1713,13 +1744,33 @@ extern "C" int ffmoe_gemm_wgrad_shared(const void* a_, const void* b_, const int
     a.xB = static_cast<const bf16_t*>(shared->b);
     a.xC = static_cast<bf16_t*>(shared->c);
     a.x_rows = static_cast<int>(shared->rows);
-    a.total_tiles += static_cast<int64_t>(a.m_tiles) * a.n_tiles;
-    a.lpt = E + 1 <= kLptMaxE;
+    // A dense group's tiles take K = all of its rows, where a routed
+    // expert's take K = its share; from kPairMinRows rows on its K is cut in
+    // two halves (two groups, each tile finished by whichever half arrives
+    // second, through the persistent GEMMs' workspace), so its tiles are no
+    // longer the launch's long pole.  Each cut tile moves a 256 KiB fp32
+    // partial, small against the >= 2 MiB of operands a half reads.
+    constexpr int kPairMinRows = 4096;
+    const int P = a.m_tiles * a.n_tiles;
+    const int G = sk_blocks();
+    int groups = 1;
+    if (sk_workspace != nullptr && a.x_rows >= kPairMinRows && G > 0 && 2 * G < kPairKey && P <= kPairMax &&
+        P <= 2 * G) {
+      groups = 2;
+      a.x_split = 2;
+      a.x_chunk = ((a.x_rows + 1) / 2 + 63) / 64 * 64;
+      a.flags = static_cast<int*>(sk_workspace);
+      a.part = reinterpret_cast<float*>(static_cast<char*>(sk_workspace) + kSkFlagBytes);
+      a.pub_off = kPairPubOff;
+      a.err_idx = 2 * G;
+    }
+    a.total_tiles += static_cast<int64_t>(groups) * P;
+    a.lpt = E + groups <= kLptMaxE;
   }
   return launch<BM, BN, false, false, 1, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_wgrad");
 }
 
 extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
                                 int Nc, void* c_out, void* stream) {
-  return ffmoe_gemm_wgrad_shared(a_, b_, offsets, E, M, Nc, c_out, nullptr, stream);
+  return ffmoe_gemm_wgrad_shared(a_, b_, offsets, E, M, Nc, c_out, nullptr, nullptr, stream);
 }

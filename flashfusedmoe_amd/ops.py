@@ -343,11 +343,11 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     # routing backward just wrote are cache-resident (measured 0.5% faster per
     # C2 step than after the dX GEMMs)
     dwd = torch.empty(E, D, H, dtype=_BF16, device=dev)
+    ws = L.ptr(L.gemm_workspace(dev, st))
     L.call("ffmoe_gemm_wgrad_shared", L.ptr(wgo), L.ptr(act), L.ptr(offsets), E, D, H, L.ptr(dwd),
-           _byref(g_wd), st)
+           _byref(g_wd), ws, st)
     gup = torch.empty(T, H2, dtype=_BF16, device=dev)
     tr = L.gemm_tile_rows(T, E)
-    ws = L.ptr(L.gemm_workspace(dev, st))
     L.call("ffmoe_gemm_dgrad_glu_shared", L.ptr(wgo), L.ptr(w_down), L.ptr(up), L.ptr(offsets),
            L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(gup), _byref(g_dg), ws, st)
     # the up-projection weight gradient right after the GEMM that wrote `gup`
@@ -355,7 +355,7 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     # per step than after the dX GEMMs
     dwu = torch.empty(E, H2, D, dtype=_BF16, device=dev)
     L.call("ffmoe_gemm_wgrad_shared", L.ptr(gup), L.ptr(xs), L.ptr(offsets), E, H2, D, L.ptr(dwu),
-           _byref(g_wu), st)
+           _byref(g_wu), ws, st)
     ghb = torch.empty(T, D, dtype=_BF16, device=dev)
     L.call("ffmoe_gemm_dgrad_shared", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr,
            E, T, H, D, L.ptr(ghb), _byref(g_dx), ws, st)

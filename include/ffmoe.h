@@ -220,8 +220,14 @@ int ffmoe_gemm_dgrad_shared(const void* gup, const void* w_up, const int32_t* of
                             const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
                             int H, int D, void* ghb_out, const ffmoe_dense_group* shared,
                             void* sk_workspace, void* stream);
+/* ffmoe_gemm_wgrad_shared: with sk_workspace (the persistent GEMMs'
+ * workspace, ffmoe_gemm_workspace_bytes) and a dense group of at least 4096
+ * rows, the group's K is cut into two halves finished through the
+ * workspace (the sum of the two fp32 halves: the same bits whichever half
+ * finishes first); NULL keeps one K range per tile. */
 int ffmoe_gemm_wgrad_shared(const void* a, const void* b, const int32_t* offsets, int E, int M,
-                            int Nc, void* c_out, const ffmoe_dense_group* shared, void* stream);
+                            int Nc, void* c_out, const ffmoe_dense_group* shared,
+                            void* sk_workspace, void* stream);
 
 /* Reports a failed stream-K partner wait of an earlier grouped GEMM on
  * sk_workspace.  The wait is bounded; it is not expected to time out (the

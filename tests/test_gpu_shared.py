@@ -11,6 +11,8 @@ kernels as one dense row group with the GLU fused into the epilogues.
   CPU (_GLUFFN.forward), every parameter gradient within the bf16 tolerance.
 """
 
+import ctypes
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -122,3 +124,59 @@ def test_moelayer_shared_expert_forward_backward(act, D, ffn, fold):
         ref = getattr(sh, name).weight.grad
         check_close(grads[f"shared_expert.{name}.weight"], ref, f"grad shared {name}",
                     atol=2e-3 * max(1.0, ref.abs().max().item()))
+
+
+@pytest.mark.parametrize("rows,split", [(5000, True), (4095, False), (300, False)])
+def test_wgrad_dense_group_split_k(rows, split):
+    """ffmoe_gemm_wgrad_shared with the persistent GEMMs' workspace: a dense
+    group of >= 4096 rows has its K cut into two halves (here 2560 + 2440
+    rows), each tile finished by the half that arrives second.  Checked
+    against fp64 (routed experts and the dense group), bit-identical over
+    two calls (the two fp32 halves are added in either order: the same
+    bits), and without the workspace (one K range) to within bf16
+    rounding of the output.  The routed experts' outputs are unaffected."""
+    from flashfusedmoe_amd import _lib as L
+    g = torch.Generator().manual_seed(rows)
+    E, M, Nc = 4, 512, 768
+    counts = torch.tensor([700, 0, 1300, 333])
+    offs = torch.zeros(E + 1, dtype=torch.int32)
+    offs[1:] = torch.cumsum(counts, 0)
+    T = int(offs[-1])
+    a = torch.randn(T, M, generator=g).to(torch.bfloat16)
+    b = torch.randn(T, Nc, generator=g).to(torch.bfloat16)
+    xa = torch.randn(rows, M, generator=g).to(torch.bfloat16)
+    xb = torch.randn(rows, Nc, generator=g).to(torch.bfloat16)
+    dev = torch.device("cuda")
+    a_d, b_d, xa_d, xb_d, offs_d = (t.to(dev) for t in (a, b, xa, xb, offs))
+    st = L.stream_ptr(dev)
+    ws = L.gemm_workspace(dev, st)
+
+    def run(workspace):
+        c = torch.empty(E, M, Nc, dtype=torch.bfloat16, device=dev)
+        xc = torch.empty(M, Nc, dtype=torch.bfloat16, device=dev)
+        grp = L.dense_group(xa_d, xb_d, xc, rows, 0)
+        L.call("ffmoe_gemm_wgrad_shared", L.ptr(a_d), L.ptr(b_d), L.ptr(offs_d), E, M, Nc, L.ptr(c),
+               ctypes.byref(grp), workspace, st)
+        return c, xc
+
+    c1, x1 = run(L.ptr(ws))
+    c2, x2 = run(L.ptr(ws))
+    c0, x0 = run(None)
+    L.check_gemm_workspaces()  # no cut tile's wait timed out; flags left clear
+    torch.cuda.synchronize()
+    assert torch.equal(x1, x2) and torch.equal(c1, c2)
+    assert torch.equal(c1, c0)  # routed experts: same kernel path either way
+    f = torch.float64
+    exp_x = xa.to(f).t() @ xb.to(f)
+    check_close(x1, exp_x, "dense group (split)" if split else "dense group")
+    for e in range(E):
+        lo, hi = int(offs[e]), int(offs[e + 1])
+        exp = a[lo:hi].to(f).t() @ b[lo:hi].to(f)
+        if hi > lo:
+            check_close(c1[e], exp, f"expert {e}")
+    d = (x1.double() - x0.double()).abs()
+    if split:  # different fp32 summation grouping: at most bf16 rounding apart
+        assert (d <= 2.0 ** -7 * x0.double().abs() + 1e-2).all()
+    else:
+        assert torch.equal(x1, x0)
+    assert not ws[:8192].any()  # the cut-tile counters and publications were cleared
