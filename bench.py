@@ -58,7 +58,9 @@ STEP_KERNELS = {
     "ffmoe_permute": ["permute"],
     "ffmoe_gemm_up_glu": ["gemm_up_glu"],
     "ffmoe_gemm_down": ["gemm_down"],
-    "ffmoe_combine": ["combine"],
+    "ffmoe_combine": ["combine", "dx_combine"],  # E > 32: the backward's dX gather is a combine
+    "ffmoe_gate_logits": ["gate_logits"],
+    "ffmoe_gate_dx": ["gate_dx"],
     "ffmoe_route_bwd_ex": ["route_bwd"],
     "ffmoe_gemm_wgrad": ["gemm_wgrad_down", "gemm_wgrad_up"],
     "ffmoe_gemm_dgrad_glu": ["gemm_dgrad_glu"],
@@ -68,7 +70,25 @@ STEP_KERNELS = {
 }
 # what each bandwidth kernel is in the reference's vocabulary
 HBM_ROLES = {"permute": "scatter", "combine": "combine", "route_bwd": "weighted scatter",
-             "dx_reduce": "gather", "route_fwd": "route"}
+             "dx_reduce": "gather", "dx_combine": "gather", "route_fwd": "route"}
+
+
+def kernel_rates(in_step, work):
+    """{kernel: {in_step_ms, rate, unit, frac}} from in-step durations and
+    algorithmic work (flop: vs the bf16 MFMA peak; byte: vs HBM)."""
+    kernels = {}
+    for name, ms_in in sorted(in_step.items()):
+        w, kind = work.get(name, (None, "byte"))
+        ent = {"in_step_ms": round(ms_in, 5)}
+        if w is not None:
+            if kind == "flop":
+                rate = w / (ms_in * 1e-3) / 1e12
+                ent.update(rate=round(rate, 2), unit="TFLOP/s", frac=round(rate / PEAK_BF16_TFLOPS, 4))
+            else:
+                rate = w / (ms_in * 1e-3) / 1e9
+                ent.update(rate=round(rate, 1), unit="GB/s", frac=round(rate / PEAK_HBM_GBS, 4))
+        kernels[name] = ent
+    return kernels
 
 
 def make_inputs(N, D, ffn, E, seed=0):
@@ -108,6 +128,10 @@ def algorithmic_work(c, rows):
         # dX gather: ghb rows read, dx written, gl and gate for the gate term
         "dx_reduce": (rows * D * b + N * D * b + N * E * b + E * D * b + T * 4, "byte"),
         "gate_grad": (N * D * b + N * E * b + E * D * b, "byte"),
+        # E > 32: dX as a combine of ghb rows plus the gl.gate addend
+        "dx_combine": (rows * D * b + 2 * N * D * b + T * 4, "byte"),
+        "gate_logits": (2.0 * N * D * E, "flop"),
+        "gate_dx": (2.0 * N * E * D, "flop"),
     }
 
 
@@ -451,6 +475,11 @@ def traffic_summary(fetch_csv, write_csv, out_path, commands):
         ratio = f"{tb / a:.2f}" if a else "-"
         lines.append(f"| {name} | {fetch[name]:.0f} | {write[name]:.0f} | {tb} | {a if a else '-'} | {ratio} |")
         mach.append(f"traffic_bytes {name} {tb}")
+    low = [(n, (fetch[n] * sf + write[n] * sw) * 1024 / alg[n]) for n in TRAFFIC_ORDER if alg.get(n)]
+    low = [(n, r) for n, r in low if r < 0.9]
+    if low:
+        lines += ["", "Below the algorithmic bytes (the counters miss part of what these kernels must move,",
+                  "so their figure is a lower bound): " + ", ".join(f"{n} ({r:.2f})" for n, r in low) + "."]
     lines += ["", "Machine-readable (read by bench.py for `traffic`):", "", "```", *mach, "```", ""]
     with open(out_path, "w") as f:
         f.write("\n".join(lines))
@@ -479,8 +508,11 @@ def stats_summary(prof_dir, bench_log, out_path, title, command):
     for ln in open(bench_log):
         if ln.startswith("{"):
             line = json.loads(ln)
-    gemm = [r["Kernel_Name"] for r in trace if "ffmoe::gemm_" in r["Kernel_Name"]]
-    role_sym = dict(zip(GEMM_STEP_ORDER, gemm[:len(GEMM_STEP_ORDER)]))
+    # the grouped GEMMs only (not the dense gate GEMMs or their split-K reduce)
+    gemm = [r["Kernel_Name"] for r in trace
+            if "ffmoe::gemm_" in r["Kernel_Name"] and "dense" not in r["Kernel_Name"]]
+    order = GEMM_STEP_ORDER[:2] if (line or {}).get("pass") == "fwd" else GEMM_STEP_ORDER
+    role_sym = dict(zip(order, gemm[:len(order)]))
     total = sum(float(r["TotalDurationNs"]) for r in stats)
     out = [f"# rocprofv3 kernel statistics: {title}", "",
            "Command (from the repository root on one MI355X):", "", "```", command, "```", "",
@@ -492,7 +524,7 @@ def stats_summary(prof_dir, bench_log, out_path, title, command):
                    f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
                    f"{float(r['Percentage']):.2f} |")
     out += ["", "Kernel symbol of each grouped GEMM of the step (the first step's GEMM dispatches):", ""]
-    for role in GEMM_STEP_ORDER:
+    for role in order:
         sym = role_sym.get(role, "?")
         durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace
                 if r["Kernel_Name"] == sym]
@@ -512,6 +544,18 @@ def stats_summary(prof_dir, bench_log, out_path, title, command):
             out.append(f"rocprofv3's average over the {st['Calls']} launches of its symbol in this run: "
                        f"{float(st['AverageNs']) / 1e3:.2f} us.")
         out.append(f"Step time of this run: {line['ms_per_step']} ms ({line['value']} tokens/s).")
+    elif line is not None:
+        out += ["", f"Step time of this run: {line['ms_per_step']} ms ({line.get('tokens_per_s')} tokens/s, "
+                    f"{line.get('expert_tflops')} TFLOP/s of expert GEMMs)."]
+        if line.get("kernels"):
+            out += ["", "In-step durations from the same run (HIP events around each launch):", "",
+                    "| Kernel | in-step ms | rate |", "|---|---:|---:|"]
+            for n, k in line["kernels"].items():
+                rate = f"{k['rate']} {k['unit']} ({k['frac'] * 100:.1f}%)" if "rate" in k else "-"
+                if "weight_stream" in k:
+                    w = k["weight_stream"]
+                    rate += f"; operand + output bytes at {w['rate']} GB/s ({w['frac'] * 100:.1f}% of HBM)"
+                out.append(f"| {n} | {k['in_step_ms']} | {rate} |")
     out.append("")
     with open(out_path, "w") as f:
         f.write("\n".join(out))
@@ -599,17 +643,7 @@ def main():
         work = algorithmic_work(c, rows)
         flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         traffic = measured_traffic()
-        for name, ms_in in sorted(in_step.items()):
-            w, kind = work.get(name, (None, "byte"))
-            ent = {"in_step_ms": round(ms_in, 5)}
-            if w is not None:
-                if kind == "flop":
-                    rate = w / (ms_in * 1e-3) / 1e12
-                    ent.update(rate=round(rate, 2), unit="TFLOP/s", frac=round(rate / PEAK_BF16_TFLOPS, 4))
-                else:
-                    rate = w / (ms_in * 1e-3) / 1e9
-                    ent.update(rate=round(rate, 1), unit="GB/s", frac=round(rate / PEAK_HBM_GBS, 4))
-            kernels[name] = ent
+        kernels = kernel_rates(in_step, work)
         gemms = [n for n in kernels if n.startswith("gemm_")]
         if gemms:
             dom = max(gemms, key=lambda n: kernels[n]["in_step_ms"])
@@ -620,7 +654,7 @@ def main():
                             timing="in-step: HIP events around every launch of "
                                    f"{args.instr_steps} instrumented fwd+bwd steps")
         for name, role in HBM_ROLES.items():
-            if name not in kernels:
+            if name not in kernels or name not in fns:
                 continue
             w = work[name][0]
             cold = cold_launch_ms(fns[name], flush, 20)

@@ -47,7 +47,8 @@ def zipf_bias(E, s=1.1, seed=4):
     return 2.0 * torch.log(pz / pz.sum())
 
 
-def run(name, cfg, steps, warmup):
+def run(name, cfg, steps, warmup, instr_steps=3):
+    import bench
     from flashfusedmoe_amd import fused_moe
     N, D, ffn, E, k, std = (cfg[key] for key in ("N", "D", "ffn", "E", "k", "std"))
     H = ffn // 2
@@ -85,11 +86,31 @@ def run(name, cfg, steps, warmup):
     ms = ev0.elapsed_time(ev1) / steps
     T = N * k
     flop = (2.0 * T * D * 2 * H + 2.0 * T * H * D) * (3 if cfg["bwd"] else 1)
+    # in-step durations of every kernel (HIP events around each launch of a
+    # few more steps), rated against the MFMA or HBM peak; nothing is
+    # dropped here (max_tokens_per_expert = N*k), so every entry is a row
+    in_step = bench.instrumented_steps(step, instr_steps)
+    work = bench.algorithmic_work(cfg, T)
+    if "gate_logits" in in_step:  # the route kernel reads the logits, not x and the gate
+        work["route_fwd"] = (N * E * 2 + T * 12, "byte")
+    kernels = bench.kernel_rates(in_step, work)
+    # few rows per expert (C3's decode, C5's 128) make the expert GEMMs stream
+    # their weights (or, for the wgrads, write them): rate each GEMM's operand
+    # + output bytes against HBM as well
+    for n, b in bench.algorithmic_bytes(cfg, T).items():
+        if n.startswith("gemm_") and n in kernels:
+            r = b / (kernels[n]["in_step_ms"] * 1e-3) / 1e9
+            kernels[n]["weight_stream"] = {"bytes": int(b), "rate": round(r, 1), "unit": "GB/s",
+                                           "frac": round(r / bench.PEAK_HBM_GBS, 4)}
+    hbm = {n: dict(role=role, bound="hbm", achieved=kernels[n]["rate"], peak=bench.PEAK_HBM_GBS,
+                   unit="GB/s", frac=kernels[n]["frac"], timing="in-step")
+           for n, role in bench.HBM_ROLES.items() if n in kernels and "rate" in kernels[n]}
     print(json.dumps({
         "config": name, "pass": "fwd+bwd" if cfg["bwd"] else "fwd", "ms_per_step": round(ms, 4),
         "tokens_per_s": round(N / (ms * 1e-3), 1), "expert_tflops": round(flop / (ms * 1e-3) / 1e12, 2),
         "steps": steps, "warmup": warmup, "dtype": "bf16", "data": "synthetic",
         "shape": {key: cfg[key] for key in ("N", "D", "ffn", "E", "k")}, "wall_s_timed": round(wall, 3),
+        "hbm_rooflines": hbm, "kernels": kernels,
     }), flush=True)
     del x, gate, wu, wd, go, leaves
     torch.cuda.empty_cache()

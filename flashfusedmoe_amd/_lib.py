@@ -67,6 +67,16 @@ SIGNATURES = {
     "ffmoe_route_bwd_ex": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I, _I, _I,
                                 _I, _P, _P, _I, _F, _P, _P, _P, _P]),
     "ffmoe_glu_fwd": (_I, [_P, _L, _I, _I, _P, _P]),
+    "ffmoe_t_gemm_dense": (_I, [_I, _I, _I, _P, _P, _P, _I, _I, _I, _L, _L, _L, _I, _P]),
+    "ffmoe_t_gemm_rows": (_I, [_I, _P, _P, _P, _P, _I, _L, _I, _I, _I, _P, _P]),
+    "ffmoe_t_gemm_wgrad": (_I, [_I, _P, _P, _P, _I, _I, _I, _P, _P]),
+    "ffmoe_t_glu_fwd": (_I, [_I, _P, _L, _I, _I, _I, _P, _P]),
+    "ffmoe_t_glu_bwd": (_I, [_I, _P, _P, _L, _I, _I, _I, _P, _P]),
+    "ffmoe_t_permute": (_I, [_I, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "ffmoe_t_combine": (_I, [_I, _P, _P, _P, _P, _L, _I, _I, _P, _P]),
+    "ffmoe_t_route_bwd": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I, _I,
+                               _I, _I, _P, _P, _I, _F, _P, _P, _P, _P]),
+    "ffmoe_route_logits_f32": (_I, [_P, _P, _I, _F, _I, _I, _L, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "ffmoe_glu_bwd": (_I, [_P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_scatter_rows": (_I, [_P, _P, _P, _L, _I, _I, _L, _P, _P]),
     "ffmoe_routing_scatter_padded": (_I, [_P, _P, _P, _P, _L, _I, _I, _L, _I, _L, _P, _P, _P]),

@@ -23,6 +23,7 @@ UNITS = (
     *((("route.hip", f"route_et{et}.o", (f"-DFFMOE_ROUTE_PART={et}",)) for et in (1, 2, 4, 8, 16))),
     ("combine.hip", "combine.o", ()),
     ("gemm.hip", "gemm.o", ()),
+    ("generic.hip", "generic.o", ()),
 )
 ARCH = os.environ.get("FFMOE_ARCH", "gfx950")
 

@@ -336,23 +336,34 @@ struct AuxRoute {
 
 // Routing backward, one wave per token n:
 //   g_w[s] = <down[src_s], go[n]> (fp32)                 fused_moe.py:527-535
-//   wgo[row_s] = bf16(go[n] * bf16(w_s)) for owned rows   moe_ops.py:248-288
+//   wgo[row_s] = T(go[n] * T(w_s)) for owned rows         moe_ops.py:248-288
 //   g_tl = softmax / sigmoid top-k backward               fused_moe.py:573-584
 //   gl[n,:] = scatter(g_tl) + d z_loss/dl + d aux/dl       :587-588, :1178-1194
-template <int KMAX>
+// T is the compute dtype: bf16 (16-byte vectors, bf16 logits) or fp32 /
+// fp64 (element-wise, fp32 logits: the reference's top-k and losses read
+// logits.float()); products and the top-k backward are fp32 either way, as
+// the reference's Triton kernels and fp32 routing tensors are.
+template <typename T> struct LogitOf { using type = float; };
+template <> struct LogitOf<bf16_t> { using type = bf16_t; };
+__device__ __forceinline__ float to_f32(bf16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(double v) { return static_cast<float>(v); }
+template <typename T> __device__ __forceinline__ T from_f32(float f) { return static_cast<T>(f); }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float f) { return f32_to_bf16(f); }
+
+template <int KMAX, typename T = bf16_t>
 __global__ __launch_bounds__(256) void route_bwd_kernel(
-    const bf16_t* __restrict__ go, const bf16_t* __restrict__ down,
+    const T* __restrict__ go, const T* __restrict__ down,
     const int32_t* __restrict__ row_of, const int64_t* __restrict__ topk_idx,
-    const float* __restrict__ topk_w, const bf16_t* __restrict__ logits,
+    const float* __restrict__ topk_w, const typename LogitOf<T>::type* __restrict__ logits,
     const float* __restrict__ lse, const int32_t* __restrict__ counts,
     const float* __restrict__ g_aux, const float* __restrict__ g_z, float aux_coeff, float z_coeff,
     int64_t N, int D, int E, int k, int gating, int capacity_mode, AuxRoute ar,
-    bf16_t* __restrict__ wgo, bf16_t* __restrict__ gl, float* __restrict__ grad_w) {
+    T* __restrict__ wgo, T* __restrict__ gl, float* __restrict__ grad_w) {
+  constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
   const int lane = threadIdx.x & 63;
   const int64_t n = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (n >= N) return;
-  const int nvec = D / 8;
-  const uint4* gor = reinterpret_cast<const uint4*>(go + n * D);
   // every slot's row index and weight first; then, per chunk of VC vectors
   // per lane, the go vectors and every slot's down vectors are all in flight
   // before the first product (per slot, the lane still adds its vectors in
@@ -372,9 +383,21 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
       rsrc[s] = src_row(rowv[s]);
       const float w = topk_w[n * k + s];
       wsum += w;
-      wb[s] = round_bf16(w);
+      wb[s] = kBf16 ? round_bf16(w) : w;  // topk_w.to(dtype), then fp32 in the kernel
     }
   }
+  if constexpr (!kBf16) {
+    for (int d = lane; d < D; d += 64) {
+      const float g = to_f32(go[n * D + d]);
+#pragma unroll
+      for (int s = 0; s < KMAX; ++s) {
+        if (rsrc[s] >= 0) dot[s] += to_f32(down[static_cast<int64_t>(rsrc[s]) * D + d]) * g;
+        if (rowv[s] >= 0) wgo[static_cast<int64_t>(rowv[s]) * D + d] = static_cast<T>(g * wb[s]);
+      }
+    }
+  } else {
+  const int nvec = D / 8;
+  const uint4* gor = reinterpret_cast<const uint4*>(go + n * D);
   for (int v0 = lane; v0 < nvec; v0 += 64 * VC) {
     uint4 gv[VC], dv[KMAX][VC];
 #pragma unroll
@@ -410,6 +433,7 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
       }
     }
   }
+  }
 #pragma unroll
   for (int s = 0; s < KMAX; ++s) gw[s] = s < k ? wave_sum(dot[s]) : 0.0f;
   if (capacity_mode && !(wsum > 0.0f)) {
@@ -433,7 +457,7 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
 #pragma unroll
     for (int s = 0; s < KMAX; ++s) {
       if (s < k) {
-        const float l = bf16_to_f32(logits[n * E + topk_idx[n * k + s]]);
+        const float l = to_f32(logits[n * E + topk_idx[n * k + s]]);
         ts[s] = 1.0f / (1.0f + expf(-l));
         tsum += ts[s];
         gdw += gw[s] * topk_w[n * k + s];
@@ -478,7 +502,7 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
       if (s < k) {
         aux_ids[s] = static_cast<int>(ai[n * k + s]);
         ga[s] = A * (static_cast<float>(ac[aux_ids[s]]) / static_cast<float>(N));
-        l[s] = bf16_to_f32(logits[n * E + aux_ids[s]]);
+        l[s] = to_f32(logits[n * E + aux_ids[s]]);
         mx = fmaxf(mx, l[s]);
       }
     }
@@ -534,18 +558,18 @@ __global__ __launch_bounds__(256) void route_bwd_kernel(
 #pragma unroll
         for (int s = 0; s < KMAX; ++s)
           if (s < k && aux_ids[s] == e) dp += aux_dp[s];
-        g += expf(bf16_to_f32(logits[n * E + e]) - lse[n]) * (dp - aux_t);
+        g += expf(to_f32(logits[n * E + e]) - lse[n]) * (dp - aux_t);
       }
     }
     if (zc != 0.0f || ac != 0.0f) {
-      const float l = bf16_to_f32(logits[n * E + e]);
+      const float l = to_f32(logits[n * E + e]);
       if (zc != 0.0f) g += zc * expf(l - lse[n]);
       if (ac != 0.0f) {
         const float sg = 1.0f / (1.0f + expf(-l));
         g += ac * (static_cast<float>(counts[e]) / static_cast<float>(N)) * sg * (1.0f - sg);
       }
     }
-    gl[n * E + e] = f32_to_bf16(g);
+    gl[n * E + e] = from_f32<T>(g);
   }
 }
 
@@ -846,6 +870,52 @@ static int route_bwd_impl(const void* go, const void* down, const int32_t* row_o
   if (check_launch("route_bwd_kernel")) return 1;
   return clear_error();
 }
+
+namespace ffmoe {
+
+template <typename T>
+static void route_bwd_t_k(int k, dim3 grid, hipStream_t st, const void* go, const void* down,
+                          const int32_t* row_of, const int64_t* topk_idx, const float* topk_w,
+                          const float* logits, const float* lse, const int32_t* counts, const float* g_aux,
+                          const float* g_z, float aux_coeff, float z_coeff, int64_t N, int D, int E,
+                          int gating, int capacity_mode, const AuxRoute& ar, void* wgo, void* gl,
+                          float* grad_w) {
+#define FFMOE_RBT(KM)                                                                                 \
+  hipLaunchKernelGGL((route_bwd_kernel<KM, T>), grid, dim3(256), 0, st, static_cast<const T*>(go),    \
+                     static_cast<const T*>(down), row_of, topk_idx, topk_w, logits, lse, counts, g_aux, \
+                     g_z, aux_coeff, z_coeff, N, D, E, k, gating, capacity_mode, ar,                   \
+                     static_cast<T*>(wgo), static_cast<T*>(gl), grad_w)
+  if (k <= 2)
+    FFMOE_RBT(2);
+  else if (k <= 4)
+    FFMOE_RBT(4);
+  else if (k <= 8)
+    FFMOE_RBT(8);
+  else
+    FFMOE_RBT(16);
+#undef FFMOE_RBT
+}
+
+int route_bwd_t_launch(int dtype, const void* go, const void* down, const int32_t* row_of,
+                       const int64_t* topk_idx, const float* topk_w, const float* logits, const float* lse,
+                       const int32_t* counts, const float* g_aux, const float* g_z, float aux_coeff,
+                       float z_coeff, int64_t N, int D, int E, int k, int gating, int capacity_mode,
+                       int aux_through, const int64_t* aux_idx, const int32_t* aux_counts, int pre_softmax,
+                       float scoring, void* wgo, void* gl, float* grad_w, hipStream_t st) {
+  if (g_aux != nullptr && counts == nullptr) return set_error("ffmoe_t_route_bwd: counts required");
+  const AuxRoute ar{aux_through, aux_idx, aux_counts, pre_softmax, scoring};
+  const dim3 grid(static_cast<unsigned>((N + 3) / 4));
+  if (dtype == FFMOE_DTYPE_F32)
+    route_bwd_t_k<float>(k, grid, st, go, down, row_of, topk_idx, topk_w, logits, lse, counts, g_aux, g_z,
+                         aux_coeff, z_coeff, N, D, E, gating, capacity_mode, ar, wgo, gl, grad_w);
+  else
+    route_bwd_t_k<double>(k, grid, st, go, down, row_of, topk_idx, topk_w, logits, lse, counts, g_aux, g_z,
+                          aux_coeff, z_coeff, N, D, E, gating, capacity_mode, ar, wgo, gl, grad_w);
+  if (check_launch("route_bwd_kernel")) return 1;
+  return clear_error();
+}
+
+}  // namespace ffmoe
 
 extern "C" int ffmoe_route_bwd(const void* go, const void* down, const int32_t* row_of,
                                const int64_t* topk_idx, const float* topk_w, const void* logits,

@@ -91,18 +91,30 @@ struct TopK {
   }
 };
 
-template <int ET, int KMAX, bool FROM_LOGITS>
+// Logits source of the route kernel: the fused MFMA gate GEMM (bf16), bf16
+// logits from memory, or fp32 logits from memory (the fp32 / fp64 compute
+// path: the reference's top-k and losses read logits.float(),
+// fused_topk.py:52, fused_moe.py:1191).
+enum LogitSrc { kGateGemm = 0, kLogitsBf16 = 1, kLogitsF32 = 2 };
+__device__ __forceinline__ float logit_f32(bf16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ float logit_f32(float v) { return v; }
+
+template <int ET, int KMAX, int SRC>
 __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ gate,
-    const bf16_t* __restrict__ logits_in, RouteOpts o, int64_t N, int D,
+    const void* __restrict__ logits_in_v, RouteOpts o, int64_t N, int D,
     int E, int k, int gating, int need_ssum, bf16_t* __restrict__ logits_out,
     int64_t* __restrict__ topk_idx, float* __restrict__ topk_w, float* __restrict__ lse_out,
     int32_t* __restrict__ rank_local, RouteWs ws) {
+  constexpr bool FROM_LOGITS = SRC != kGateGemm;
+  using LT = typename std::conditional<SRC == kLogitsF32, float, bf16_t>::type;
+  constexpr int LV = 16 / sizeof(LT);  // logits per 16-byte load
+  const LT* __restrict__ logits_in = static_cast<const LT*>(logits_in_v);
   constexpr int EP = ET * 16;        // padded expert count
-  constexpr int LS = EP + 2;         // LDS row stride (bf16 elements)
+  constexpr int LS = EP + 4 / sizeof(LT);  // LDS row stride (elements): rows 4 bytes apart from 16-byte alignment
   extern __shared__ float smem[];
-  bf16_t* L = reinterpret_cast<bf16_t*>(smem);       // [64][LS] bf16 logits
-  int* sel_i = reinterpret_cast<int*>(smem + kRouteTokens * LS / 2);  // [64*k]
+  LT* L = reinterpret_cast<LT*>(smem);       // [64][LS] logits
+  int* sel_i = reinterpret_cast<int*>(smem + kRouteTokens * LS * sizeof(LT) / 4);  // [64*k]
   float* sel_w = reinterpret_cast<float*>(sel_i + kRouteTokens * k);  // [64*k]
   float* zl = sel_w + kRouteTokens * k;              // [64]
 
@@ -114,17 +126,17 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
   const int ntok = static_cast<int>(min<int64_t>(kRouteTokens, N - tok_base));
 
   if constexpr (FROM_LOGITS) {
-    if (E % 8 == 0) {
+    if (E % LV == 0) {
       // 16-byte loads, all of a thread's in flight before the first LDS
-      // write (logits rows are 16-byte aligned when E % 8 == 0; the LDS
+      // write (logits rows are 16-byte aligned when E % LV == 0; the LDS
       // rows, padded by 4 bytes, take them as four 4-byte writes)
-      constexpr int NV = kRouteTokens * EP / 8;
+      constexpr int NV = kRouteTokens * EP / LV;
       constexpr int PER = (NV + kRouteThreads - 1) / kRouteThreads;
       uint4 v[PER];
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int p = i * kRouteThreads + tid;
-        const int t = p / (EP / 8), e = (p % (EP / 8)) * 8;
+        const int t = p / (EP / LV), e = (p % (EP / LV)) * LV;
         v[i] = make_uint4(0, 0, 0, 0);
         if (p < NV && t < ntok && e < E)
           v[i] = *reinterpret_cast<const uint4*>(logits_in + (tok_base + t) * E + e);
@@ -132,7 +144,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int p = i * kRouteThreads + tid;
-        const int t = p / (EP / 8), e = (p % (EP / 8)) * 8;
+        const int t = p / (EP / LV), e = (p % (EP / LV)) * LV;
         if (p < NV) {
           uint32_t* d = reinterpret_cast<uint32_t*>(L + t * LS + e);
           d[0] = v[i].x;
@@ -144,12 +156,12 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     } else {
       for (int p = tid; p < kRouteTokens * EP; p += kRouteThreads) {
         const int t = p / EP, e = p % EP;
-        bf16_t v = 0;
+        LT v = 0;
         if (t < ntok && e < E) v = logits_in[(tok_base + t) * E + e];
         L[t * LS + e] = v;
       }
     }
-  } else {
+  } else if constexpr (SRC == kGateGemm) {
     // Wave `wave` computes logits of tokens [16*wave, 16*wave+16) against all
     // experts with v_mfma_f32_16x16x32_bf16: A = x rows (K-contiguous),
     // B = gate rows (K-contiguous).  Lane l holds row l%16, k-block l/16.
@@ -227,7 +239,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
       for (int r = 0; r < 4; ++r) {
         const int tl = 16 * wave + 4 * (lane >> 4) + r;
         const bf16_t h = f32_to_bf16(acc[t][r]);
-        L[tl * LS + e] = h;
+        L[tl * LS + e] = static_cast<LT>(h);
         if (logits_out != nullptr && tl < ntok && e < E)
           logits_out[(tok_base + tl) * E + e] = h;
       }
@@ -247,14 +259,14 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     static_assert(LPT == 4, "four lanes per token");
     const int t = tid / LPT, jl = tid % LPT;
     const bool tok_ok = t < ntok;
-    const bf16_t* lr = L + t * LS;
+    const LT* lr = L + t * LS;
     float lse = 0.0f;
     // logsumexp of the logits (z-loss and the pre-softmax probabilities)
     float m = -INFINITY, s = 0.0f;
     if (tok_ok) {
 #pragma unroll 8
       for (int e = jl; e < E; e += LPT) {
-        const float l = bf16_to_f32(lr[e]);
+        const float l = logit_f32(lr[e]);
         if (l > m) {
           s = s * expf(m - l) + 1.0f;
           m = l;
@@ -276,13 +288,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     float psum = 0.0f;  // pre-softmax: sum of exp(l - max)
     if (o.pre_softmax) {
       if (tok_ok)
-        for (int e = jl; e < E; e += LPT) psum += expf(bf16_to_f32(lr[e]) - m);
+        for (int e = jl; e < E; e += LPT) psum += expf(logit_f32(lr[e]) - m);
 #pragma unroll
       for (int off = 1; off < LPT; off <<= 1) psum += __shfl_xor(psum, off, kWave);
     }
     // selection score of expert e (fused_moe.py:144-200)
     auto score = [&](int e) {
-      const float l = bf16_to_f32(lr[e]);
+      const float l = logit_f32(lr[e]);
       float sc;
       if (gating == FFMOE_GATING_SOFTMAX)
         sc = o.pre_softmax ? expf(l - m) / psum : l;
@@ -302,7 +314,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
         const int per = k / o.topk_group;
         // bf16 selection scores (softmax logits, unbiased or with a bf16 bias)
         // are summed in fp32 and rounded to bf16, as torch sums a bf16 tensor
-        const bool bf16_scores = gating == FFMOE_GATING_SOFTMAX && !o.pre_softmax &&
+        const bool bf16_scores = SRC != kLogitsF32 && gating == FFMOE_GATING_SOFTMAX && !o.pre_softmax &&
                                  (o.bias == nullptr || o.bias_round);
         TopK<FFMOE_MAX_TOPK> tg;
         tg.init();
@@ -358,11 +370,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
         float mx = -INFINITY;
 #pragma unroll
         for (int q = 0; q < KMAX; ++q)
-          if (q < k) mx = fmaxf(mx, bf16_to_f32(lr[tk.i[q]]));
+          if (q < k) mx = fmaxf(mx, logit_f32(lr[tk.i[q]]));
 #pragma unroll
         for (int q = 0; q < KMAX; ++q) {
           if (q < k) {
-            w[q] = expf(bf16_to_f32(lr[tk.i[q]]) - mx);
+            w[q] = expf(logit_f32(lr[tk.i[q]]) - mx);
             wsum += w[q];
           }
         }
@@ -374,7 +386,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
 #pragma unroll
         for (int q = 0; q < KMAX; ++q) {
           if (q < k) {
-            const float l = bf16_to_f32(lr[tk.i[q]]);
+            const float l = logit_f32(lr[tk.i[q]]);
             w[q] = (gating == FFMOE_GATING_SOFTMAX) ? expf(l - m) / psum : 1.0f / (1.0f + expf(-l));
             wsum += w[q];
           }
@@ -418,7 +430,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_fwd_kernel(
     ws.psum[blk * E + e] = ps;
     if (need_ssum) {
       float ss = 0.0f;
-      for (int t = 0; t < ntok; ++t) ss += 1.0f / (1.0f + expf(-bf16_to_f32(L[t * LS + e])));
+      for (int t = 0; t < ntok; ++t) ss += 1.0f / (1.0f + expf(-logit_f32(L[t * LS + e])));
       ws.ssum[blk * E + e] = ss;
     }
   };
@@ -742,13 +754,13 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
 constexpr int kPermTokens = 8;  // tokens per permute block
 
 // Resolves each entry's row (block base + block-local rank), renormalises the
-// kept weights in capacity mode, and copies each token row once from HBM to
-// each of its k destination rows.
+// kept weights in capacity mode, and copies each token row (nvec 16-byte
+// vectors: any element type) once from HBM to each of its k destination rows.
 __global__ __launch_bounds__(256) void permute_kernel(
-    const bf16_t* __restrict__ x, const int64_t* __restrict__ topk_idx, float* __restrict__ topk_w,
+    const uint4* __restrict__ x, const int64_t* __restrict__ topk_idx, float* __restrict__ topk_w,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ rank_local, const int32_t* __restrict__ base, int64_t N, int D,
-    int E, int k, int mt, int capacity_mode, bf16_t* __restrict__ xs, int32_t* __restrict__ row_of) {
+    const int32_t* __restrict__ rank_local, const int32_t* __restrict__ base, int64_t N, int nvec,
+    int E, int k, int mt, int capacity_mode, uint4* __restrict__ xs, int32_t* __restrict__ row_of) {
   __shared__ int s_row[kPermTokens * FFMOE_MAX_TOPK];
   const int tid = threadIdx.x;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kPermTokens;
@@ -785,44 +797,46 @@ __global__ __launch_bounds__(256) void permute_kernel(
       topk_w[n * k + q] = w / den;
     }
   }
-  const int nvec = D / 8;
   for (int p = tid; p < ntok * nvec; p += blockDim.x) {
     const int t = p / nvec, v = p % nvec;
-    const uint4 val = reinterpret_cast<const uint4*>(x + (t0 + t) * static_cast<int64_t>(D))[v];
+    const uint4 val = x[(t0 + t) * static_cast<int64_t>(nvec) + v];
     for (int q = 0; q < k; ++q) {
       const int row = s_row[t * k + q];
-      if (row >= 0) reinterpret_cast<uint4*>(xs + static_cast<int64_t>(row) * D)[v] = val;
+      if (row >= 0) xs[static_cast<int64_t>(row) * nvec + v] = val;
     }
   }
 }
 
 #endif  // FFMOE_ROUTE_PART == 0
 
-template <int ET, int KMAX, bool FL>
+template <int ET, int KMAX, int SRC>
 static void launch_route(dim3 grid, size_t shm, hipStream_t st, const bf16_t* x, const bf16_t* gate,
-                         const bf16_t* li, const RouteOpts& o, int64_t N, int D, int E, int k,
+                         const void* li, const RouteOpts& o, int64_t N, int D, int E, int k,
                          int gating, int need_ssum, bf16_t* lo, int64_t* ti, float* tw, float* lse,
                          int32_t* rl, RouteWs ws) {
-  hipLaunchKernelGGL((route_fwd_kernel<ET, KMAX, FL>), grid, dim3(kRouteThreads), shm, st, x, gate,
+  hipLaunchKernelGGL((route_fwd_kernel<ET, KMAX, SRC>), grid, dim3(kRouteThreads), shm, st, x, gate,
                      li, o, N, D, E, k, gating, need_ssum, lo, ti, tw, lse, rl, ws);
 }
 
 template <int ET, int KMAX>
-static void launch_route_fl(bool fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
-                            const bf16_t* gate, const bf16_t* li, const RouteOpts& o, int64_t N,
+static void launch_route_fl(int src, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
+                            const bf16_t* gate, const void* li, const RouteOpts& o, int64_t N,
                             int D, int E, int k, int gating, int need_ssum, bf16_t* lo, int64_t* ti,
                             float* tw, float* lse, int32_t* rl, RouteWs ws) {
-  if (fl)
-    launch_route<ET, KMAX, true>(grid, shm, st, x, gate, li, o, N, D, E, k, gating, need_ssum,
-                                 lo, ti, tw, lse, rl, ws);
+  if (src == kLogitsBf16)
+    launch_route<ET, KMAX, kLogitsBf16>(grid, shm, st, x, gate, li, o, N, D, E, k, gating, need_ssum,
+                                        lo, ti, tw, lse, rl, ws);
+  else if (src == kLogitsF32)
+    launch_route<ET, KMAX, kLogitsF32>(grid, shm, st, x, gate, li, o, N, D, E, k, gating, need_ssum,
+                                       lo, ti, tw, lse, rl, ws);
   else
-    launch_route<ET, KMAX, false>(grid, shm, st, x, gate, li, o, N, D, E, k, gating, need_ssum,
-                                  lo, ti, tw, lse, rl, ws);
+    launch_route<ET, KMAX, kGateGemm>(grid, shm, st, x, gate, li, o, N, D, E, k, gating, need_ssum,
+                                      lo, ti, tw, lse, rl, ws);
 }
 
 template <int ET>
-void launch_route_k(int k, bool fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
-                           const bf16_t* gate, const bf16_t* li, const RouteOpts& o, int64_t N,
+void launch_route_k(int k, int fl, dim3 grid, size_t shm, hipStream_t st, const bf16_t* x,
+                           const bf16_t* gate, const void* li, const RouteOpts& o, int64_t N,
                            int D, int E, int gating, int need_ssum, bf16_t* lo, int64_t* ti,
                            float* tw, float* lse, int32_t* rl, RouteWs ws) {
 #define FFMOE_RK(KM)                                                                           \
@@ -843,8 +857,8 @@ void launch_route_k(int k, bool fl, dim3 grid, size_t shm, hipStream_t st, const
 // is compiled in a translation unit of its own (FFMOE_ROUTE_PART = ET), in
 // parallel, and part 0 holds everything else.
 #define FFMOE_ROUTE_K_INST(ETV)                                                                     \
-  template void launch_route_k<ETV>(int, bool, dim3, size_t, hipStream_t, const bf16_t*,         \
-                                    const bf16_t*, const bf16_t*, const RouteOpts&, int64_t, int, \
+  template void launch_route_k<ETV>(int, int, dim3, size_t, hipStream_t, const bf16_t*,          \
+                                    const bf16_t*, const void*, const RouteOpts&, int64_t, int,   \
                                     int, int, int, bf16_t*, int64_t*, float*, float*, int32_t*,    \
                                     RouteWs)
 #if FFMOE_ROUTE_PART > 0
@@ -879,7 +893,7 @@ extern "C" size_t ffmoe_route_workspace_bytes(int64_t N, int E, int k) {
 static int route_fwd_impl(const void* x, const void* gate, const void* logits_in, RouteOpts o,
                           int64_t N, int D, int E, int k, int gating, int need_sigmoid_sum,
                           void* logits_out, int64_t* topk_idx, float* topk_w, float* lse,
-                          void* workspace, void* stream) {
+                          void* workspace, void* stream, bool logits_f32 = false) {
   if (N <= 0) return set_error("ffmoe_route_fwd: N must be positive");
   if (E < 1 || E > FFMOE_MAX_EXPERTS) return set_error("ffmoe_route_fwd: E out of range [1, 256]");
   if (k < 1 || k > E || k > FFMOE_MAX_TOPK)
@@ -903,17 +917,18 @@ static int route_fwd_impl(const void* x, const void* gate, const void* logits_in
     return set_error("ffmoe_route_fwd: input jitter needs the gate GEMM (no logits_in)");
   if (gating != FFMOE_GATING_SOFTMAX) o.pre_softmax = 0;  // the reference ignores it there
   const int ET = E <= 16 ? 1 : E <= 32 ? 2 : E <= 64 ? 4 : E <= 128 ? 8 : 16;
-  const int LS = ET * 16 + 2;  // bf16 elements per LDS logits row
-  const size_t shm = static_cast<size_t>(kRouteTokens) * LS * 2 +
+  const size_t lsz = logits_f32 ? 4 : 2;
+  const int LS = ET * 16 + static_cast<int>(4 / lsz);  // logits per LDS row (rows padded by 4 bytes)
+  const size_t shm = static_cast<size_t>(kRouteTokens) * LS * lsz +
                      (2 * static_cast<size_t>(kRouteTokens) * k + kRouteTokens) * 4;
   RouteWs ws = route_ws(workspace, N, E);
   int32_t* rl = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + rank_local_offset(N, E));
   const dim3 grid(static_cast<unsigned>(route_blocks(N)));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool fl = logits_in != nullptr;
+  const int fl = logits_in == nullptr ? kGateGemm : (logits_f32 ? kLogitsF32 : kLogitsBf16);
   auto xb = static_cast<const bf16_t*>(x);
   auto gb = static_cast<const bf16_t*>(gate);
-  auto lb = static_cast<const bf16_t*>(logits_in);
+  const void* lb = logits_in;
   auto lo = static_cast<bf16_t*>(logits_out);
 #define FFMOE_RE(ETV)                                                                           \
   launch_route_k<ETV>(k, fl, grid, shm, st, xb, gb, lb, o, N, D, E, gating, need_sigmoid_sum,   \
@@ -953,6 +968,16 @@ extern "C" int ffmoe_route_fwd_ex(const void* x, const void* gate, const void* l
                         topk_idx, topk_w, lse, workspace, stream);
 }
 
+extern "C" int ffmoe_route_logits_f32(const float* logits, const float* expert_bias, int pre_softmax,
+                                      float scoring_factor, int n_group, int topk_group, int64_t N, int E,
+                                      int k, int gating, int need_sigmoid_sum, int64_t* topk_idx,
+                                      float* topk_w, float* lse, void* workspace, void* stream) {
+  if (logits == nullptr) return set_error("ffmoe_route_logits_f32: null logits");
+  RouteOpts o{expert_bias, 0, pre_softmax, scoring_factor, n_group, topk_group, nullptr};
+  return route_fwd_impl(nullptr, nullptr, logits, o, N, 0, E, k, gating, need_sigmoid_sum, nullptr, topk_idx,
+                        topk_w, lse, workspace, stream, true);
+}
+
 extern "C" int ffmoe_route_scan(int64_t N, int E, int k, int mt, int gemm_bm, float aux_coeff,
                                 float z_coeff, int gating, void* workspace, int32_t* counts,
                                 int32_t* offsets, int32_t* tile_offsets, float* stats,
@@ -973,22 +998,44 @@ extern "C" int ffmoe_route_scan(int64_t N, int E, int k, int mt, int gemm_bm, fl
   return clear_error();
 }
 
-extern "C" int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
-                             const int32_t* offsets, const int32_t* counts, int64_t N, int D, int E,
-                             int k, int mt, int capacity_mode, void* workspace, void* x_sorted,
-                             int32_t* row_of, void* stream) {
-  if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_permute: D must be a positive multiple of 8");
+static int permute_impl(const void* x, const int64_t* topk_idx, float* topk_w, const int32_t* offsets,
+                        const int32_t* counts, int64_t N, int64_t row_bytes, int E, int k, int mt,
+                        int capacity_mode, void* workspace, void* x_sorted, int32_t* row_of, void* stream,
+                        const char* name) {
+  if (N <= 0 || row_bytes <= 0 || row_bytes % 16 != 0 || row_bytes / 16 > 0x7fffffff)
+    return set_error(std::string(name) + ": rows must be a positive multiple of 16 bytes");
   if (k < 1 || k > FFMOE_MAX_TOPK || E < 1 || E > FFMOE_MAX_EXPERTS)
-    return set_error("ffmoe_permute: bad k/E");
+    return set_error(std::string(name) + ": bad k/E");
   RouteWs ws = route_ws(workspace, N, E);
   const int32_t* rl =
       reinterpret_cast<const int32_t*>(static_cast<char*>(workspace) + rank_local_offset(N, E));
   const dim3 grid(static_cast<unsigned>((N + kPermTokens - 1) / kPermTokens));
   hipLaunchKernelGGL(permute_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const bf16_t*>(x), topk_idx, topk_w, offsets, counts, rl, ws.hist,
-                     N, D, E, k, mt, capacity_mode, static_cast<bf16_t*>(x_sorted), row_of);
+                     static_cast<const uint4*>(x), topk_idx, topk_w, offsets, counts, rl, ws.hist, N,
+                     static_cast<int>(row_bytes / 16), E, k, mt, capacity_mode, static_cast<uint4*>(x_sorted),
+                     row_of);
   if (check_launch("permute_kernel")) return 1;
   return clear_error();
+}
+
+extern "C" int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
+                             const int32_t* offsets, const int32_t* counts, int64_t N, int D, int E,
+                             int k, int mt, int capacity_mode, void* workspace, void* x_sorted,
+                             int32_t* row_of, void* stream) {
+  if (D <= 0 || D % 8 != 0) return set_error("ffmoe_permute: D must be a positive multiple of 8");
+  return permute_impl(x, topk_idx, topk_w, offsets, counts, N, static_cast<int64_t>(D) * 2, E, k, mt,
+                      capacity_mode, workspace, x_sorted, row_of, stream, "ffmoe_permute");
+}
+
+extern "C" int ffmoe_t_permute(int dtype, const void* x, const int64_t* topk_idx, float* topk_w,
+                               const int32_t* offsets, const int32_t* counts, int64_t N, int D, int E,
+                               int k, int mt, int capacity_mode, void* workspace, void* x_sorted,
+                               int32_t* row_of, void* stream) {
+  const int es = dtype == FFMOE_DTYPE_F32 ? 4 : dtype == FFMOE_DTYPE_F64 ? 8 : 0;
+  if (es == 0) return set_error("ffmoe_t_permute: dtype must be FFMOE_DTYPE_F32 or FFMOE_DTYPE_F64");
+  if (D <= 0 || D % 8 != 0) return set_error("ffmoe_t_permute: D must be a positive multiple of 8");
+  return permute_impl(x, topk_idx, topk_w, offsets, counts, N, static_cast<int64_t>(D) * es, E, k, mt,
+                      capacity_mode, workspace, x_sorted, row_of, stream, "ffmoe_t_permute");
 }
 
 #endif  // FFMOE_ROUTE_PART == 0

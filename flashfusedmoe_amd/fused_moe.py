@@ -3,8 +3,12 @@
 Drop-in for the reference's non-expert-parallel ``fused_moe``
 (src/flashfusemoe/fused_moe.py:1073-1246): same signature and defaults, same
 validation messages, same losses dict, same overflow error.  Every step runs
-as a hand-written HIP kernel behind libffmoe.so (see ops.py); bfloat16 is the
-compute dtype (directly, or through ``torch.autocast(dtype=torch.bfloat16)``).
+as a hand-written HIP kernel behind libffmoe.so (see ops.py).  The compute
+dtype is the reference's: the autocast dtype if autocast is on, else the
+input dtype.  bfloat16 runs on the MFMA pipeline; float32 and float64 run
+on this library's fp32 / fp64 kernels with the reference's fp32 internals
+(routing on logits.float(), GLU and gather sums in fp32); float16 is not
+supported and raises.
 
 Layout differences that are invisible through this API: expert rows are
 stored compactly (no [E, max_tokens] padding rows are allocated or computed),
@@ -72,6 +76,16 @@ def _compute_dtype(fallback):
     return fallback
 
 
+SUPPORTED_DTYPES = (torch.bfloat16, torch.float32, torch.float64)
+
+
+def _check_compute_dtype(dtype):
+    if dtype not in SUPPORTED_DTYPES:
+        raise TypeError(
+            f"ffmoe computes in bfloat16, float32 or float64; got compute dtype {dtype} (pass "
+            "tensors of one of those or run under torch.autocast('cuda', dtype=torch.bfloat16))")
+
+
 def _overflow_message(actual_max, max_tokens):
     # fused_moe.py:403-410 (same text, so callers matching on it keep working)
     return (
@@ -104,10 +118,7 @@ class _FusedMoEFunction(torch.autograd.Function):
         N, D = x.shape
         E = gate.shape[0]
         dtype = _compute_dtype(x.dtype)
-        if dtype != torch.bfloat16:
-            raise TypeError(
-                f"ffmoe computes in bfloat16; got compute dtype {dtype} (pass bf16 tensors "
-                "or run under torch.autocast('cuda', dtype=torch.bfloat16))")
+        _check_compute_dtype(dtype)
         xc = x.to(dtype).contiguous()
         gc = gate.to(dtype).contiguous()
         wu = w_up.to(dtype).contiguous()
@@ -124,7 +135,7 @@ class _FusedMoEFunction(torch.autograd.Function):
         act_id = L.ACTIVATION[activation]
         need_ssum = gating == "sigmoid" and aux_coeff > 0.0
         # a bf16 bias is added to the bf16 logits in bf16 (fused_moe.py:176)
-        bias_round = (expert_bias is not None and expert_bias.dtype == torch.bfloat16
+        bias_round = (dtype == torch.bfloat16 and expert_bias is not None and expert_bias.dtype == torch.bfloat16
                       and gating == "softmax" and not pre_softmax)
         ropts = (bool(bias_round), bool(pre_softmax), float(scoring or 0.0), int(n_group or 0),
                  int(topk_group or 0))
@@ -199,7 +210,7 @@ class _FusedMoEFunction(torch.autograd.Function):
         aux_through, pre_softmax, scoring = ctx.rcfg
         if grad_out is None:
             grad_out = torch.zeros_like(xc)
-        go = grad_out.to(torch.bfloat16).contiguous()
+        go = grad_out.to(xc.dtype).contiguous()
         ga = g_aux if (ctx.aux_has_grad and aux_coeff > 0.0) else None
         gz = g_z if z_coeff > 0.0 else None
         # the sigmoid aux gradient's expert fractions come from the losses

@@ -16,7 +16,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .fused_moe import _compute_dtype, fused_moe
+from .fused_moe import _check_compute_dtype, _compute_dtype, fused_moe
 
 # the shared expert's activations (nn.py:33-40); its GeGLU is the exact erf
 # GELU of F.gelu, unlike the routed experts' tanh form
@@ -32,10 +32,7 @@ class _SharedGLU(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w_gate, w_up, w_down, act_id):
         dtype = _compute_dtype(x.dtype)
-        if dtype != torch.bfloat16:
-            raise TypeError(
-                f"ffmoe computes in bfloat16; got compute dtype {dtype} (pass bf16 tensors "
-                "or run under torch.autocast('cuda', dtype=torch.bfloat16))")
+        _check_compute_dtype(dtype)
         xc = x.to(dtype).contiguous()
         w_gu = torch.cat([w_gate.to(dtype), w_up.to(dtype)], 0).contiguous()
         wd = w_down.to(dtype).contiguous()
@@ -48,7 +45,7 @@ class _SharedGLU(torch.autograd.Function):
     @staticmethod
     def backward(ctx, go):
         xc, w_gu, wd, up, act = ctx.saved_tensors
-        dx, dwgu, dwd = ops.dense_glu_backward(go.to(torch.bfloat16).contiguous(), xc, w_gu, wd,
+        dx, dwgu, dwd = ops.dense_glu_backward(go.to(xc.dtype).contiguous(), xc, w_gu, wd,
                                                up, act, ctx.act_id)
         H = wd.shape[1]
         xd, gd, ud, dd = ctx.dtypes
@@ -85,6 +82,11 @@ class MoELayer(nn.Module):
     """Fused Mixture-of-Experts layer (nn.py:47-176).
 
     Returns (output, losses); losses is empty unless aux/z losses are on.
+    Computes in the autocast dtype, else the input dtype: bfloat16 on the
+    MFMA kernels (the shared expert folded into the routed GEMM launches
+    when d_model and ffn_dim/2 are multiples of 64), float32 / float64 on the
+    fp32 / fp64 kernels (the default fp32 parameters without autocast);
+    float16 raises TypeError.
     """
 
     def __init__(
@@ -152,7 +154,8 @@ class MoELayer(nn.Module):
         # the shared expert runs inside the routed GEMM launches (a dense row
         # group) when its dimensions suit the direct-to-LDS pipeline; else
         # as its own dense GEMMs after the routed op
-        fold = se is not None and D % 64 == 0 and self.half_ffn % 64 == 0
+        fold = (se is not None and _compute_dtype(x.dtype) == torch.bfloat16 and D % 64 == 0
+                and self.half_ffn % 64 == 0)
         shared = None
         if fold:
             shared = (se.w_gate.weight, se.w_up.weight, se.w_down.weight, _SHARED_ACT[se.activation])

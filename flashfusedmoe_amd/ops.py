@@ -4,7 +4,10 @@ Each op enqueues HIP kernels on the current stream through the C ABI of
 include/ffmoe.h and allocates its outputs with the torch caching allocator.
 Fake (meta) implementations make the ops traceable by torch.compile.
 
-Only bfloat16 CUDA(ROCm) tensors are accepted; there is no other path.
+The compute dtype is bfloat16 (the MFMA pipeline) or float32 / float64 (the
+reference's computation in the input dtype, on this library's fp32 / fp64
+kernels, ffmoe_t_* in include/ffmoe.h).  Tensors must be on a ROCm GPU;
+there is no CPU path.
 """
 
 import ctypes
@@ -25,6 +28,22 @@ _CHECK_GEMM = os.environ.get("FFMOE_CHECK_GEMM", "0") not in ("", "0")
 def _require(cond, msg):
     if not cond:
         raise ValueError(msg)
+
+
+# compute dtypes of the fp32 / fp64 path -> FFMOE_DTYPE_* codes
+T_DTYPES = {torch.float32: 1, torch.float64: 2}
+# row tile of the fp32 / fp64 grouped GEMM (ffmoe_t_gemm_rows)
+T_TILE_ROWS = 64
+
+
+def _check_t_gpu(name, t, dtype):
+    if t.device.type != "cuda":
+        raise RuntimeError(f"ffmoe: {name} must be on a ROCm GPU (got {t.device}); "
+                           "the fused MoE kernels have no CPU path")
+    if t.dtype != dtype:
+        raise TypeError(f"ffmoe: {name} must be {dtype} like the hidden states (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"ffmoe: {name} must be contiguous")
 
 
 def _check_bf16_gpu(name, t):
@@ -123,7 +142,12 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
     [E+1], stats fp32 [4], istats int32 [4], workspace uint8, aux_loss fp32 [],
     z_loss fp32 []] (the two losses repeat stats[AUX] and stats[Z] as
     separate tensors).  bias_round / pre_softmax / scoring / n_group /
-    topk_group / noise are ffmoe_route_fwd_ex's routing options."""
+    topk_group / noise are ffmoe_route_fwd_ex's routing options.  With fp32
+    / fp64 hidden states the logits are fp32 (x gate^T in the dtype, then
+    rounded as the reference's logits.float()) and bias_round is unused."""
+    if x.dtype in T_DTYPES:
+        return _route_t(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, need_ssum,
+                        pre_softmax, scoring, n_group, topk_group, noise)
     _check_bf16_gpu("hidden_states", x)
     _check_bf16_gpu("gate_weight", gate)
     N, D = x.shape
@@ -167,6 +191,47 @@ def route(x: Tensor, gate: Tensor, expert_bias: Optional[Tensor], top_k: int, ga
     return [logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats, ws, aux, z]
 
 
+def _route_t(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, need_ssum, pre_softmax,
+             scoring, n_group, topk_group, noise):
+    """route() for fp32 / fp64 hidden states: the gate product in the dtype
+    (fp32 output), the route kernel on the fp32 logits, the scan with the
+    fp32 / fp64 GEMM's 64-row tiles."""
+    _check_t_gpu("hidden_states", x, x.dtype)
+    _check_t_gpu("gate_weight", gate, x.dtype)
+    dt = T_DTYPES[x.dtype]
+    N, D = x.shape
+    E = gate.shape[0]
+    k = top_k
+    dev = x.device
+    f32 = torch.float32
+    ws = torch.empty(L.route_workspace_bytes(N, E, k), dtype=torch.uint8, device=dev)
+    logits = torch.empty(N, E, dtype=f32, device=dev)
+    topk_idx = torch.empty(N, k, dtype=torch.int64, device=dev)
+    topk_w = torch.empty(N, k, dtype=f32, device=dev)
+    lse = torch.empty(N, dtype=f32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    tile_offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    stats = torch.empty(L.NUM_STATS, dtype=f32, device=dev)
+    istats = torch.empty(L.NUM_ISTATS, dtype=torch.int32, device=dev)
+    aux = torch.empty((), dtype=f32, device=dev)
+    z = torch.empty((), dtype=f32, device=dev)
+    bias = None if expert_bias is None else expert_bias.to(device=dev, dtype=f32).contiguous()
+    st = L.stream_ptr(dev)
+    xin = x
+    if noise is not None:  # (x * noise) gate^T in the dtype (fused_moe.py:329-332)
+        _check_t_gpu("input jitter noise", noise, x.dtype)
+        xin = x * noise
+    L.call("ffmoe_t_gemm_dense", dt, 0, 1, L.ptr(xin), L.ptr(gate), L.ptr(logits), N, E, D, D, D, E, 1, st)
+    L.call("ffmoe_route_logits_f32", L.ptr(logits), L.ptr(bias), int(pre_softmax), float(scoring),
+           int(n_group), int(topk_group), N, E, k, gating, int(need_ssum), L.ptr(topk_idx), L.ptr(topk_w),
+           L.ptr(lse), L.ptr(ws), st)
+    L.call("ffmoe_route_scan", N, E, k, mt, T_TILE_ROWS, aux_coeff, z_coeff, gating, L.ptr(ws),
+           L.ptr(counts), L.ptr(offsets), L.ptr(tile_offsets), L.ptr(stats), L.ptr(istats), L.ptr(aux),
+           L.ptr(z), st)
+    return [logits, topk_idx, topk_w, lse, counts, offsets, tile_offsets, stats, istats, ws, aux, z]
+
+
 @route.register_fake
 def _route_fake(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, need_ssum,
                 bias_round=False, pre_softmax=False, scoring=0.0, n_group=0, topk_group=0,
@@ -174,7 +239,7 @@ def _route_fake(x, gate, expert_bias, top_k, gating, mt, aux_coeff, z_coeff, nee
     N, D = x.shape
     E = gate.shape[0]
     f = lambda *s, dtype: x.new_empty(s, dtype=dtype)  # noqa: E731
-    return [f(N, E, dtype=_BF16), f(N, top_k, dtype=torch.int64), f(N, top_k, dtype=torch.float32),
+    return [f(N, E, dtype=_BF16 if x.dtype == _BF16 else torch.float32), f(N, top_k, dtype=torch.int64), f(N, top_k, dtype=torch.float32),
             f(N, dtype=torch.float32), f(E, dtype=torch.int32), f(E + 1, dtype=torch.int32),
             f(E + 1, dtype=torch.int32), f(L.NUM_STATS, dtype=torch.float32),
             f(L.NUM_ISTATS, dtype=torch.int32), f(0, dtype=torch.uint8), f(dtype=torch.float32),
@@ -231,7 +296,12 @@ def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, t
     shared_w_gu [2H,D] (gate rows, then up rows) and shared_w_down [D,H] the
     shared expert runs as a dense row group of the same GEMM launches and
     `out` is bf16(routed + shared) (nn.py:156-159); up_sh / act_sh are its
-    pre-activation and activation (empty without it)."""
+    pre-activation and activation (empty without it).  fp32 / fp64 x: the
+    fp32 / fp64 kernels (no shared-expert group there)."""
+    if x.dtype in T_DTYPES:
+        _require(shared_w_gu is None, "the shared-expert group runs on the bf16 path only")
+        return _experts_forward_t(x, w_up, w_down, topk_idx, topk_w, counts, offsets, tile_offsets, ws,
+                                  top_k, activation, mt, capacity_mode, save_activations)
     _check_bf16_gpu("w_up", w_up)
     _check_bf16_gpu("w_down", w_down)
     N, D = x.shape
@@ -264,6 +334,52 @@ def experts_forward(x: Tensor, w_up: Tensor, w_down: Tensor, topk_idx: Tensor, t
     if not save_activations:
         return [out, tw_out, row_of, xs, empty, empty.clone(), empty.clone(), *sh_out]
     return [out, tw_out, row_of, xs, up, act, down, *sh_out]
+
+
+def _up_down_t(xs, w_up, w_down, offsets, tile_offsets, activation, st):
+    """fp32 / fp64 routed up product, GLU (fp32 math), down product."""
+    dt = T_DTYPES[xs.dtype]
+    T, D = xs.shape
+    E, H2, _ = w_up.shape
+    H = H2 // 2
+    e = lambda *s: xs.new_empty(s)  # noqa: E731
+    up, act, down = e(T, H2), e(T, H), e(T, D)
+    P = L.ptr
+    L.call("ffmoe_t_gemm_rows", dt, P(xs), P(w_up), P(offsets), P(tile_offsets), E, T, D, H2, 0, P(up), st)
+    L.call("ffmoe_t_glu_fwd", dt, P(up), T, H, activation, 0, P(act), st)
+    L.call("ffmoe_t_gemm_rows", dt, P(act), P(w_down), P(offsets), P(tile_offsets), E, T, H, D, 0, P(down), st)
+    return up, act, down
+
+
+def _experts_forward_t(x, w_up, w_down, topk_idx, topk_w, counts, offsets, tile_offsets, ws, top_k,
+                       activation, mt, capacity_mode, save_activations):
+    """experts_forward() in fp32 / fp64: the same permutation and combine
+    order as the bf16 path; products in the dtype, GLU and combine sums in
+    fp32 stored in the dtype (activations.py:58-74, moe_ops.py:190-203)."""
+    dtype = x.dtype
+    for name, t in (("hidden_states", x), ("w_up", w_up), ("w_down", w_down)):
+        _check_t_gpu(name, t, dtype)
+    dt = T_DTYPES[dtype]
+    N, D = x.shape
+    E = w_up.shape[0]
+    k = top_k
+    T = N * k
+    dev = x.device
+    st = L.stream_ptr(dev)
+    P = L.ptr
+    tw = topk_w.clone() if capacity_mode else topk_w
+    xs = torch.empty(T, D, dtype=dtype, device=dev)
+    row_of = torch.empty(T, dtype=torch.int32, device=dev)
+    L.call("ffmoe_t_permute", dt, P(x), P(topk_idx), P(tw), P(offsets), P(counts), N, D, E, k, mt,
+           int(capacity_mode), P(ws), P(xs), P(row_of), st)
+    up, act, down = _up_down_t(xs, w_up, w_down, offsets, tile_offsets, activation, st)
+    out = torch.empty(N, D, dtype=dtype, device=dev)
+    L.call("ffmoe_t_combine", dt, P(down), P(row_of), P(tw), None, N, D, k, P(out), st)
+    tw_out = tw if capacity_mode else topk_w.new_empty(0)
+    empty = x.new_empty(0)
+    if not save_activations:
+        up, act, down = empty, empty.clone(), empty.clone()
+    return [out, tw_out, row_of, xs, up, act, down, empty.clone(), empty.clone()]
 
 
 @experts_forward.register_fake
@@ -306,7 +422,13 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     aux_* describe the aux loss's own routing (ffmoe_route_bwd_ex).  With the
     shared expert (its weights and saved up_sh / act_sh) its four GEMMs run as
     a dense row group of the routed launches, and grad_hidden includes its
-    input gradient."""
+    input gradient.  fp32 / fp64 x: the fp32 / fp64 kernels (logits fp32)."""
+    if x.dtype in T_DTYPES:
+        _require(shared_w_gu is None, "the shared-expert group runs on the bf16 path only")
+        return _experts_backward_t(go, x, gate, w_up, w_down, logits, topk_idx, topk_w, lse, counts,
+                                   offsets, tile_offsets, row_of, xs, up, act, down, g_aux, g_z, top_k,
+                                   activation, gating, capacity_mode, aux_coeff, z_coeff,
+                                   aux_through_weights, aux_idx, aux_counts, pre_softmax, scoring)
     _check_bf16_gpu("grad_output", go)
     N, D = x.shape
     E, H2, _ = w_up.shape
@@ -378,6 +500,52 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     return [dx + dx_sh, dgate, dwu, dwd, dw_gu_sh, dw_sd_sh]
 
 
+def _experts_backward_t(go, x, gate, w_up, w_down, logits, topk_idx, topk_w, lse, counts, offsets,
+                        tile_offsets, row_of, xs, up, act, down, g_aux, g_z, top_k, activation, gating,
+                        capacity_mode, aux_coeff, z_coeff, aux_through_weights, aux_idx, aux_counts,
+                        pre_softmax, scoring):
+    """experts_backward() in fp32 / fp64 (fused_moe.py:511-591): routing
+    backward and weighted scatter, dgrad products with the GLU backward
+    between them, the unweighted dX gather plus gl gate, the four weight
+    gradients, all products in the dtype."""
+    dtype = x.dtype
+    _check_t_gpu("grad_output", go, dtype)
+    dt = T_DTYPES[dtype]
+    N, D = x.shape
+    E, H2, _ = w_up.shape
+    H = H2 // 2
+    k = top_k
+    T = N * k
+    dev = x.device
+    st = L.stream_ptr(dev)
+    P = L.ptr
+    if up.numel() == 0:  # recompute_activations: same kernels, same bits
+        up, act, down = _up_down_t(xs, w_up, w_down, offsets, tile_offsets, activation, st)
+    e = lambda *s: x.new_empty(s)  # noqa: E731
+    wgo, gl = e(T, D), e(N, E)
+    ga = None if g_aux is None else g_aux.to(device=dev, dtype=torch.float32).contiguous()
+    gz = None if g_z is None else g_z.to(device=dev, dtype=torch.float32).contiguous()
+    L.call("ffmoe_t_route_bwd", dt, P(go), P(down), P(row_of), P(topk_idx), P(topk_w), P(logits), P(lse),
+           P(counts), P(ga), P(gz), aux_coeff, z_coeff, N, D, E, k, gating, int(capacity_mode),
+           int(aux_through_weights), P(aux_idx), P(aux_counts), int(pre_softmax), float(scoring), P(wgo),
+           P(gl), None, st)
+    gact, gup, ghb = e(T, H), e(T, H2), e(T, D)
+    L.call("ffmoe_t_gemm_rows", dt, P(wgo), P(w_down), P(offsets), P(tile_offsets), E, T, D, H, 1, P(gact), st)
+    L.call("ffmoe_t_glu_bwd", dt, P(gact), P(up), T, H, activation, 0, P(gup), st)
+    L.call("ffmoe_t_gemm_rows", dt, P(gup), P(w_up), P(offsets), P(tile_offsets), E, T, H2, D, 1, P(ghb), st)
+    dwd, dwu = e(E, D, H), e(E, H2, D)
+    L.call("ffmoe_t_gemm_wgrad", dt, P(wgo), P(act), P(offsets), E, D, H, P(dwd), st)
+    L.call("ffmoe_t_gemm_wgrad", dt, P(gup), P(xs), P(offsets), E, H2, D, P(dwu), st)
+    # grad_hidden = gather(ghb) + gl gate (fused_moe.py:556-561, :590)
+    glg, dx = e(N, D), e(N, D)
+    L.call("ffmoe_t_gemm_dense", dt, 0, 0, P(gl), P(gate), P(glg), N, D, E, E, D, D, 0, st)
+    L.call("ffmoe_t_combine", dt, P(ghb), P(row_of), None, P(glg), N, D, k, P(dx), st)
+    dgate = e(E, D)
+    L.call("ffmoe_t_gemm_dense", dt, 1, 0, P(gl), P(x), P(dgate), E, D, N, E, D, D, 0, st)
+    e0 = x.new_empty(0)
+    return [dx, dgate, dwu, dwd, e0, e0.clone()]
+
+
 @experts_backward.register_fake
 def _experts_backward_fake(go, x, gate, w_up, w_down, logits, topk_idx, topk_w, lse, counts, offsets,
                            tile_offsets, row_of, xs, up, act, down, g_aux, g_z, top_k, activation,
@@ -402,12 +570,21 @@ def _experts_backward_fake(go, x, gate, w_up, w_down, logits, topk_idx, topk_w, 
 def dense_glu_forward(x: Tensor, w_gu: Tensor, w_down: Tensor, activation: int) -> List[Tensor]:
     """x [N,D], w_gu [2H,D] (gate rows, then up rows), w_down [D,H] ->
     [out [N,D], up [N,2H] (pre-activation), act [N,H]], all bf16."""
-    for name, t in (("x", x), ("w_gate|w_up", w_gu), ("w_down", w_down)):
-        _check_bf16_gpu(name, t)
     N, D = x.shape
     H = w_down.shape[1]
     _require(w_gu.shape == (2 * H, D) and w_down.shape == (D, H), "shared expert weight shapes")
     st = L.stream_ptr(x.device)
+    if x.dtype in T_DTYPES:  # products and the GLU in the dtype, as the torch ops (nn.py:31-40)
+        for name, t in (("x", x), ("w_gate|w_up", w_gu), ("w_down", w_down)):
+            _check_t_gpu(name, t, x.dtype)
+        dt, P = T_DTYPES[x.dtype], L.ptr
+        up, act, out = x.new_empty(N, 2 * H), x.new_empty(N, H), x.new_empty(N, D)
+        L.call("ffmoe_t_gemm_dense", dt, 0, 1, P(x), P(w_gu), P(up), N, 2 * H, D, D, D, 2 * H, 0, st)
+        L.call("ffmoe_t_glu_fwd", dt, P(up), N, H, activation, 1, P(act), st)
+        L.call("ffmoe_t_gemm_dense", dt, 0, 1, P(act), P(w_down), P(out), N, D, H, H, H, D, 0, st)
+        return [out, up, act]
+    for name, t in (("x", x), ("w_gate|w_up", w_gu), ("w_down", w_down)):
+        _check_bf16_gpu(name, t)
     up = x @ w_gu.t()
     act = torch.empty(N, H, dtype=_BF16, device=x.device)
     L.call("ffmoe_glu_fwd", L.ptr(up), N, H, activation, L.ptr(act), st)
@@ -425,11 +602,22 @@ def _dense_glu_forward_fake(x, w_gu, w_down, activation):
 @torch.library.custom_op("ffmoe::dense_glu_backward", mutates_args=())
 def dense_glu_backward(go: Tensor, x: Tensor, w_gu: Tensor, w_down: Tensor, up: Tensor,
                        act: Tensor, activation: int) -> List[Tensor]:
-    """Returns [grad_x [N,D], grad_w_gu [2H,D], grad_w_down [D,H]], bf16."""
-    _check_bf16_gpu("grad_output", go)
+    """Returns [grad_x [N,D], grad_w_gu [2H,D], grad_w_down [D,H]] in x's dtype."""
     N, D = x.shape
     H = w_down.shape[1]
     st = L.stream_ptr(x.device)
+    if x.dtype in T_DTYPES:
+        _check_t_gpu("grad_output", go, x.dtype)
+        dt, P = T_DTYPES[x.dtype], L.ptr
+        gact, gup = x.new_empty(N, H), x.new_empty(N, 2 * H)
+        dx, dwgu, dwd = x.new_empty(N, D), x.new_empty(2 * H, D), x.new_empty(D, H)
+        L.call("ffmoe_t_gemm_dense", dt, 0, 0, P(go), P(w_down), P(gact), N, H, D, D, H, H, 0, st)
+        L.call("ffmoe_t_glu_bwd", dt, P(gact), P(up), N, H, activation, 1, P(gup), st)
+        L.call("ffmoe_t_gemm_dense", dt, 0, 0, P(gup), P(w_gu), P(dx), N, D, 2 * H, 2 * H, D, D, 0, st)
+        L.call("ffmoe_t_gemm_dense", dt, 1, 0, P(go), P(act), P(dwd), D, H, N, D, H, H, 0, st)
+        L.call("ffmoe_t_gemm_dense", dt, 1, 0, P(gup), P(x), P(dwgu), 2 * H, D, N, 2 * H, D, D, 0, st)
+        return [dx, dwgu, dwd]
+    _check_bf16_gpu("grad_output", go)
     gact = go @ w_down
     gup = torch.empty(N, 2 * H, dtype=_BF16, device=x.device)
     L.call("ffmoe_glu_bwd", L.ptr(gact), L.ptr(up), N, H, activation, L.ptr(gup), st)

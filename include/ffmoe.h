@@ -49,6 +49,10 @@ extern "C" {
 #define FFMOE_ACT_RELU2 2
 #define FFMOE_ACT_GEGLU_ERF 3 /* exact erf GELU (the shared expert's F.gelu, nn.py:36) */
 
+/* compute dtype of the ffmoe_t_* entry points (the fp32 / fp64 path) */
+#define FFMOE_DTYPE_F32 1
+#define FFMOE_DTYPE_F64 2
+
 /* limits enforced by the entry points */
 #define FFMOE_MAX_EXPERTS 256
 #define FFMOE_MAX_TOPK 16
@@ -418,6 +422,78 @@ int ffmoe_routing_scatter_padded(const int64_t* sorted_order, const int64_t* fla
                                  const int64_t* starts, const void* x, int64_t N, int D,
                                  int E, int64_t mt, int k, int64_t n_sorted, void* out,
                                  int64_t* e2b, void* stream);
+
+/* ---------------------------------------------------------------------
+ * fp32 / fp64 compute path.  The reference computes in the input dtype when
+ * autocast is off (fused_moe.py:93-97, :318-327): its products are torch.bmm
+ * / matmul in that dtype, its Triton kernels compute in fp32 from operands
+ * of that dtype and store that dtype.  These entry points take the dtype
+ * (FFMOE_DTYPE_F32 / FFMOE_DTYPE_F64) and operands of it; routing tensors
+ * (topk_w, lse, logits handed to routing) stay fp32 as in the reference.
+ * Accumulation is fp32 for FFMOE_DTYPE_F32 and fp64 for FFMOE_DTYPE_F64.
+ * ------------------------------------------------------------------- */
+
+/* C [M,N] (row stride ldc) = op(A) op(B), op(X) = X or X^T of a row-major X
+ * with row stride ldX: the gate logits x gate^T (fused_moe.py:334, with
+ * out_f32 = 1: fp32 logits for routing, the reference's logits.float()),
+ * gl gate and gl^T x (:590-591), and the shared expert's products
+ * (nn.py:31-40).  out_f32 = 0: C has the dtype. */
+int ffmoe_t_gemm_dense(int dtype, int trans_a, int trans_b, const void* a, const void* b, void* c,
+                       int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc, int out_f32,
+                       void* stream);
+
+/* Grouped rows: for each expert e, rows offsets[e]..offsets[e+1] of
+ * a [rows, K] times B[e] into c [rows, N]; b_kn = 0: B[e] is [N, K] (the
+ * up and down bmm's x w^T, fused_moe.py:435, :441), b_kn = 1: B[e] is
+ * [K, N] (the dgrad bmm's g w, :547, :553).  tile_offsets: the route scan's
+ * row-tile offsets for a 64-row tile (ffmoe_route_scan gemm_bm = 64). */
+int ffmoe_t_gemm_rows(int dtype, const void* a, const void* b, const int32_t* offsets,
+                      const int32_t* tile_offsets, int E, int64_t max_rows, int K, int N, int b_kn,
+                      void* c, void* stream);
+
+/* Grouped K: c[e] [M, Nc] = a[rows e]^T b[rows e] (the wgrad bmm's,
+ * fused_moe.py:564-565). */
+int ffmoe_t_gemm_wgrad(int dtype, const void* a, const void* b, const int32_t* offsets, int E, int M,
+                       int Nc, void* c, void* stream);
+
+/* GLU forward / backward over up [M, 2H] (activations.py:27-231).
+ * compute_in_dtype = 0: fp32 math (the routed experts' Triton kernels);
+ * 1: math in the dtype (the shared expert's torch ops, nn.py:33-38). */
+int ffmoe_t_glu_fwd(int dtype, const void* up, int64_t M, int H, int activation,
+                    int compute_in_dtype, void* out, void* stream);
+int ffmoe_t_glu_bwd(int dtype, const void* grad_act, const void* up, int64_t M, int H,
+                    int activation, int compute_in_dtype, void* grad_up, void* stream);
+
+/* ffmoe_permute for rows of the dtype (moe_ops.py:43-149). */
+int ffmoe_t_permute(int dtype, const void* x, const int64_t* topk_idx, float* topk_w,
+                    const int32_t* offsets, const int32_t* counts, int64_t N, int D, int E,
+                    int k, int mt, int capacity_mode, void* workspace, void* x_sorted,
+                    int32_t* row_of, void* stream);
+
+/* ffmoe_combine for the dtype: fp32 slot-order sum of w * rows (topk_w
+ * NULL: unweighted), stored in the dtype, then + addend (may be NULL) in
+ * the dtype (moe_ops.py:156-241, fused_moe.py:556-561, :590). */
+int ffmoe_t_combine(int dtype, const void* rows, const int32_t* row_of, const float* topk_w,
+                    const void* addend, int64_t N, int D, int k, void* out, void* stream);
+
+/* ffmoe_route_bwd_ex for the dtype: grad_out, down, wgo and grad_logits in
+ * the dtype, logits fp32 (fused_moe.py:527-591, moe_ops.py:248-332). */
+int ffmoe_t_route_bwd(int dtype, const void* grad_out, const void* down, const int32_t* row_of,
+                      const int64_t* topk_idx, const float* topk_w, const float* logits,
+                      const float* lse, const int32_t* counts, const float* g_aux, const float* g_z,
+                      float aux_coeff, float z_coeff, int64_t N, int D, int E, int k, int gating,
+                      int capacity_mode, int aux_through_weights, const int64_t* aux_idx,
+                      const int32_t* aux_counts, int pre_softmax, float scoring_factor, void* wgo,
+                      void* grad_logits, float* grad_topk_w, void* stream);
+
+/* ffmoe_route_fwd_ex's routing on fp32 logits [N, E] (the reference's
+ * top-k reads logits.float(), fused_topk.py:52; its losses use
+ * logits.float(), fused_moe.py:1179-1192): same options, no jitter (the
+ * caller jitters the gate product's input). */
+int ffmoe_route_logits_f32(const float* logits, const float* expert_bias, int pre_softmax,
+                           float scoring_factor, int n_group, int topk_group, int64_t N, int E,
+                           int k, int gating, int need_sigmoid_sum, int64_t* topk_idx,
+                           float* topk_w, float* lse, void* workspace, void* stream);
 
 #ifdef __cplusplus
 }

@@ -101,8 +101,14 @@ def test_cpu_tensors_have_no_fallback():
         fused_moe(*(t.bfloat16() for t in _inputs()), top_k=2)
 
 
-def test_non_bf16_compute_dtype_is_rejected():
-    with pytest.raises(TypeError, match="bfloat16"):
+def test_fp16_compute_dtype_is_rejected():
+    with pytest.raises(TypeError, match="bfloat16, float32 or float64"):
+        fused_moe(*(t.half() for t in _inputs()), top_k=2)
+
+
+def test_fp32_cpu_tensors_are_rejected_not_computed():
+    # fp32 is a supported compute dtype, but there is no CPU path
+    with pytest.raises(RuntimeError, match="no CPU path"):
         fused_moe(*_inputs(), top_k=2)
 
 
