@@ -76,6 +76,8 @@ SIGNATURES = {
     "ffmoe_t_combine": (_I, [_I, _P, _P, _P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_t_route_bwd": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _F, _L, _I, _I, _I, _I,
                                _I, _I, _P, _P, _I, _F, _P, _P, _P, _P]),
+    "ffmoe_t_routing_scatter_padded": (_I, [_I, _P, _P, _P, _P, _L, _I, _I, _L, _I, _L, _P, _P, _P]),
+    "ffmoe_t_scatter_rows": (_I, [_I, _P, _P, _P, _L, _I, _I, _L, _P, _P]),
     "ffmoe_route_logits_f32": (_I, [_P, _P, _I, _F, _I, _I, _L, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "ffmoe_glu_bwd": (_I, [_P, _P, _L, _I, _I, _P, _P]),
     "ffmoe_scatter_rows": (_I, [_P, _P, _P, _L, _I, _I, _L, _P, _P]),

@@ -696,6 +696,19 @@ extern "C" int ffmoe_routing_scatter_padded(const int64_t* sorted_order, const i
   return clear_error();
 }
 
+extern "C" int ffmoe_t_routing_scatter_padded(int dtype, const int64_t* sorted_order, const int64_t* flat_ids,
+                                              const int64_t* starts, const void* x, int64_t N, int D, int E,
+                                              int64_t mt, int k, int64_t n_sorted, void* out, int64_t* e2b,
+                                              void* stream) {
+  // a row copy: rows of D fp32 / fp64 elements are moved as 2D / 4D bf16-sized units
+  const int units = dtype == FFMOE_DTYPE_F32 ? 2 : dtype == FFMOE_DTYPE_F64 ? 4 : 0;
+  if (units == 0) return set_error("ffmoe_t_routing_scatter_padded: dtype must be FFMOE_DTYPE_F32 or FFMOE_DTYPE_F64");
+  if (D <= 0 || D % 8 != 0 || static_cast<int64_t>(D) * units > 0x7fffffff)
+    return set_error("ffmoe_t_routing_scatter_padded: D must be a positive multiple of 8");
+  return ffmoe_routing_scatter_padded(sorted_order, flat_ids, starts, x, N, D * units, E, mt, k, n_sorted, out,
+                                      e2b, stream);
+}
+
 extern "C" int ffmoe_combine(const void* rows, const int32_t* row_of, const float* topk_w,
                              const void* addend, int64_t N, int D, int k, void* out, void* stream) {
   if (N <= 0 || D <= 0 || D % 8 != 0) return set_error("ffmoe_combine: D must be a positive multiple of 8");

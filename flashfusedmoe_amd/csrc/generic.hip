@@ -287,6 +287,24 @@ __global__ __launch_bounds__(256) void combine_t_kernel(const T* __restrict__ ro
   }
 }
 
+// Padded weighted scatter for the kernel-level boundary (moe_ops.py:248-288):
+// dst[dst_row[j]] = T(fp32(src[j / k]) * w[j]) (w NULL: a copy).
+template <typename T>
+__global__ __launch_bounds__(256) void scatter_rows_t_kernel(const T* __restrict__ src, const int64_t* __restrict__ dst_row,
+                                                             const float* __restrict__ w, int64_t n_entries, int k,
+                                                             int D, int64_t dst_rows, T* __restrict__ dst) {
+  const int64_t total = n_entries * D;
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
+       u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t j = u / D;
+    const int d = static_cast<int>(u % D);
+    const int64_t r = dst_row[j];
+    if (r < 0 || r >= dst_rows) continue;
+    const T v = src[(j / k) * D + d];
+    dst[r * D + d] = w != nullptr ? static_cast<T>(static_cast<float>(v) * w[j]) : v;
+  }
+}
+
 }  // namespace
 
 // Routing-weight gradient and weighted scatter of the fp32 / fp64 path, with
@@ -467,4 +485,21 @@ extern "C" int ffmoe_t_route_bwd(int dtype, const void* grad_out, const void* do
                             aux_coeff, z_coeff, N, D, E, k, gating, capacity_mode, aux_through_weights, aux_idx,
                             aux_counts, pre_softmax, scoring_factor, wgo, grad_logits, grad_topk_w,
                             static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ffmoe_t_scatter_rows(int dtype, const void* src, const int64_t* dst_row, const float* w,
+                                    int64_t n_entries, int k, int D, int64_t dst_rows, void* dst, void* stream) {
+  if (check_dtype(dtype, "ffmoe_t_scatter_rows")) return 1;
+  if (n_entries < 0 || k < 1 || D <= 0 || dst_rows < 0 || src == nullptr || dst_row == nullptr || dst == nullptr)
+    return set_error("ffmoe_t_scatter_rows: bad arguments");
+  if (n_entries == 0) return clear_error();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n_entries * D));
+  if (dtype == FFMOE_DTYPE_F32)
+    hipLaunchKernelGGL(scatter_rows_t_kernel<float>, grid, dim3(256), 0, st, static_cast<const float*>(src), dst_row,
+                       w, n_entries, k, D, dst_rows, static_cast<float*>(dst));
+  else
+    hipLaunchKernelGGL(scatter_rows_t_kernel<double>, grid, dim3(256), 0, st, static_cast<const double*>(src),
+                       dst_row, w, n_entries, k, D, dst_rows, static_cast<double*>(dst));
+  return check_launch("scatter_rows_t_kernel") ? 1 : clear_error();
 }

@@ -486,6 +486,17 @@ int ffmoe_t_route_bwd(int dtype, const void* grad_out, const void* down, const i
                       const int32_t* aux_counts, int pre_softmax, float scoring_factor, void* wgo,
                       void* grad_logits, float* grad_topk_w, void* stream);
 
+/* The kernel-level boundary's padded scatters for the dtype: the routing
+ * scatter (a row copy, ffmoe_routing_scatter_padded) and the weighted
+ * scatter dst[dst_row[j]] = src[j / k] * w[j] computed in fp32
+ * (ffmoe_scatter_rows; moe_ops.py:43-149, :248-332). */
+int ffmoe_t_routing_scatter_padded(int dtype, const int64_t* sorted_order, const int64_t* flat_ids,
+                                   const int64_t* starts, const void* x, int64_t N, int D, int E,
+                                   int64_t mt, int k, int64_t n_sorted, void* out, int64_t* e2b,
+                                   void* stream);
+int ffmoe_t_scatter_rows(int dtype, const void* src, const int64_t* dst_row, const float* w,
+                         int64_t n_entries, int k, int D, int64_t dst_rows, void* dst, void* stream);
+
 /* ffmoe_route_fwd_ex's routing on fp32 logits [N, E] (the reference's
  * top-k reads logits.float(), fused_topk.py:52; its losses use
  * logits.float(), fused_moe.py:1179-1192): same options, no jitter (the

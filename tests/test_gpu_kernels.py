@@ -180,3 +180,49 @@ def test_fused_moe_traces_under_torch_compile():
     assert torch.equal(ez, cz)
     for a, b in zip(eg, cg):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_kernel_boundary_fp32_fp64(dtype):
+    """The kernel-level wrappers on fp32 / fp64 tensors, as the reference's
+    Triton kernels take them (fp32 math, the input dtype stored): index
+    results bit-exact, copies exact, sums and GLU within fp32 rounding of
+    the oracle's."""
+    from flashfusedmoe_amd.kernels import (activation_backward, activation_forward, fused_gather_reduce,
+                                           fused_routing_scatter, fused_topk_routing,
+                                           fused_weighted_scatter)
+    N, D, E, k = 257, 64, 8, 2
+    g = torch.Generator().manual_seed(31)
+    logits = torch.randn(N, E, generator=g).to(dtype)
+    w, idx = fused_topk_routing(logits.cuda(), "softmax", k)
+    rw, ridx = R.route(logits.float().numpy(), k, "softmax")
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+    mt = R.estimate_max_tokens(N, k, E)
+    x = torch.randn(N, D, generator=g).to(dtype)
+    sorted_order, counts, starts, _ = R.stable_permutation(ridx, E)
+    hb, e2b = fused_routing_scatter(torch.from_numpy(sorted_order).cuda(), idx.reshape(-1),
+                                    torch.from_numpy(starts).cuda(), x.cuda(), E, mt, k)
+    exp_e2b, kept = R.expand_to_batch(ridx, E, mt)
+    assert np.array_equal(e2b.cpu().numpy(), exp_e2b)
+    exp_hb = torch.zeros(E * mt, D, dtype=dtype)
+    exp_hb[torch.from_numpy(exp_e2b[kept])] = x.repeat_interleave(k, dim=0)[torch.from_numpy(kept)]
+    assert torch.equal(hb.cpu(), exp_hb)
+    batched = torch.randn(E * mt, D, generator=g).to(dtype)
+    wt = torch.from_numpy(rw).to(dtype)
+    out = fused_gather_reduce(batched.cuda(), e2b, wt.cuda(), N, k)
+    exp = F_.gather_reduce(batched, torch.from_numpy(exp_e2b), wt, N, k)
+    torch.testing.assert_close(out.cpu(), exp, rtol=1e-6, atol=1e-6)
+    go = torch.randn(N, D, generator=g).to(dtype)
+    ws = fused_weighted_scatter(go.cuda(), e2b, wt.cuda(), E, mt, k)
+    exp_ws = F_.weighted_scatter(go, torch.from_numpy(exp_e2b), wt.reshape(-1), E * mt, k,
+                                 torch.from_numpy(kept))
+    torch.testing.assert_close(ws.cpu(), exp_ws, rtol=1e-6, atol=1e-7)
+    up = (torch.randn(3, 40, 2 * 48, generator=g) * 2).to(dtype)
+    ga = torch.randn(3, 40, 48, generator=g).to(dtype)
+    for act in ("swiglu", "geglu", "relu_squared"):
+        a = activation_forward(up.cuda(), act)
+        assert a.dtype == dtype
+        torch.testing.assert_close(a.cpu(), F_.glu_forward(up, act).to(dtype), rtol=1e-5, atol=1e-6)
+        gu = activation_backward(ga.cuda(), up.cuda(), act)
+        torch.testing.assert_close(gu.cpu(), F_.glu_backward(ga, up, act).to(dtype), rtol=1e-5, atol=1e-6)
