@@ -597,6 +597,16 @@ __device__ __forceinline__ void wait_vmcnt_le(int n) {
   }
 }
 
+// Parts a stage's direct-to-LDS loads are issued in (see gemm_dl_tile).
+// Measured at C2 (in-step µs, 1 / 2 / 4 parts): three-stage 256x128 tiles
+// gain from 4 (down 99 / 99 / 96.5, dgrad+GLU 156 / 154 / 149); two-stage
+// 256x256 tiles from 2 (dgrad 161 / 155 / 173, wgrad 143 / 135 / 152),
+// except the up GEMM with its GLU epilogue (180 / 187 / 191).
+template <int BM, int BN, int EPI>
+constexpr int issue_parts() {
+  return dl_stages<BM, BN>() >= 3 ? 4 : (EPI == EPI_GLU_FWD ? 1 : 2);
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -794,20 +804,31 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   // Loads of K step `kstep` into stage buffer `buf`.  Steps past k1 are still
   // issued, with an out-of-range offset (the buffer returns zeros and moves no
   // memory), so every step has the same number of loads in flight.
-  auto issue = [&](int kstep, int buf) {
+  // A stage's loads go out in IP parts: part 0 with the last k-step of the
+  // stage before (right after the barrier that frees the buffer), parts
+  // 1..IP-1 with the next k-steps, so the LDS writes of a stage arrive spread
+  // over the step instead of in one burst.
+  constexpr int IP = issue_parts<BM, BN, EPI>();
+  static_assert(LA % IP == 0 && LB % IP == 0 && IP <= 4, "issue parts");
+  constexpr int PA = LA / IP, PB = LB / IP;
+  auto issue_part = [&](int kstep, int buf, int part) {
     bf16_t* at = smem + buf * STAGE;
     bf16_t* bt = at + A_EL;
     const bool live = kstep < k1;
 #pragma unroll
-    for (int i = 0; i < LA; ++i)
+    for (int i = part * PA; i < (part + 1) * PA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           ra, (lds_void_t*)(at + (i * kThreads + wave * 64) * 8), 16,
           live ? offa[i] + kstep * stepa : 0xFFFFFFF0u, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < LB; ++i)
+    for (int i = part * PB; i < (part + 1) * PB; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rb, (lds_void_t*)(bt + (i * kThreads + wave * 64) * 8), 16,
           live ? offb[i] + kstep * stepb : 0xFFFFFFF0u, 0, 0, 0);
+  };
+  auto issue = [&](int kstep, int buf) {
+#pragma unroll
+    for (int q = 0; q < IP; ++q) issue_part(kstep, buf, q);
   };
 
   auto tile_col = [&](int tn) {
@@ -877,9 +898,10 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   constexpr int kLoads = LA + LB;  // loads per thread per stage
   static_assert(kLoads < 64, "vmcnt range");
   static_assert((NS - 1) * kLoads < 64, "vmcnt range");
-  // prologue: stage 0 landed (the NS-1 later stages may be in flight), LDS
-  // count free
-  constexpr int kPro = (NS - 1) * kLoads;
+  // prologue: stage 0 landed (stages 1..NS-2 and part 0 of stage NS-1 may
+  // be in flight), LDS count free
+  constexpr int kPart = kLoads / IP;  // loads per thread per issue part
+  constexpr int kPro = (NS - 2) * kLoads + kPart;
   constexpr int kWaitStage0 = (kPro & 15) | ((kPro >> 4) << 14) | 0x70 | 0xF00;
   // in the loop: the next stage landed (the NS-2 after it may be in flight)
   // and this wave's LDS reads retired
@@ -900,7 +922,17 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   const int nks = k1 - k0;
   if (nks > 0) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) issue(k0 + s, s);
+    for (int s = 0; s + 1 < NS; ++s) issue(k0 + s, s);
+    issue_part(k0 + NS - 1, NS - 1, 0);
+    // the stage whose parts 1..IP-1 go out with the next k-steps
+    int pend_step = k0 + NS - 1, pend_buf = NS - 1;
+    // k-step j (0, 1, 2) of a stage issues part j + 1 of the pending stage
+    auto issue_pending = [&](int j) {
+      if constexpr (IP > 1) {
+        if (j + 1 < IP) issue_part(pend_step, pend_buf, j + 1);
+      }
+    };
+    constexpr int kSub0 = IP > 1 ? kPart : 0, kSub1 = IP > 2 ? kPart : 0, kSub2 = IP > 3 ? kPart : 0;
     __builtin_amdgcn_s_waitcnt(kWaitStage0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -915,28 +947,34 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       ready(fa0, fb0);
       read_ks(cur, 1, fa1, fb1);
       mfma_ks(fa0, fb0);
-      interleave(0);
+      issue_pending(0);
+      interleave(kSub0);
       ready(fa1, fb1);
       read_ks(cur, 2, fa0, fb0);
       mfma_ks(fa1, fb1);
-      interleave(0);
+      issue_pending(1);
+      interleave(kSub1);
       ready(fa0, fb0);
       read_ks(cur, 3, fa1, fb1);
       mfma_ks(fa0, fb0);
-      interleave(0);
+      issue_pending(2);
+      interleave(kSub2);
       ready(fa1, fb1);
       // publish the next stage; every wave's reads of this one have retired
       __builtin_amdgcn_s_waitcnt(kWaitNext);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      // refill this stage's buffer NS steps ahead, read k-step 0 of the next
-      // stage, run k-step 3 of this one
-      issue(k0 + i + NS, cur);
+      // refill this stage's buffer NS steps ahead (part 0 now, the rest with
+      // the next k-steps), read k-step 0 of the next stage, run k-step 3 of
+      // this one
+      pend_step = k0 + i + NS;
+      pend_buf = cur;
+      issue_part(pend_step, pend_buf, 0);
       const int nxt = cur + 1 == NS ? 0 : cur + 1;
       read_ks(nxt, 0, fa0, fb0);
       mfma_ks(fa1, fb1);
-      interleave(kLoads);
+      interleave(kPart);
       cur = nxt;
     }
     ready(fa0, fb0);
