@@ -919,6 +919,30 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
     }
   };
 
+  // GLU backward: the pre-activation values of the tile are loaded during
+  // the last stage's k-steps (their latency hides under its MFMAs).  Buffer
+  // loads (rows past the group read zeros), so every thread issues exactly
+  // 2 * PIT of them, after the last stage load: the wait before the epilogue
+  // can then leave them in flight (vector-memory loads complete in order).
+  constexpr int PIT = (EPI == EPI_GLU_BWD) ? glu_bwd_items<BM, BN>() : 1;
+  uint4 pre_g[PIT], pre_u[PIT];
+  auto prefetch_up = [&]() {
+    if constexpr (EPI == EPI_GLU_BWD) {
+      constexpr int CH = BN / 8;
+      const int64_t H2 = 2 * static_cast<int64_t>(p.H);
+      const int rows = max(0, min(row_end - row_begin, BM));
+      const __amdgpu_buffer_rsrc_t ru =
+          make_rsrc(p.up + static_cast<int64_t>(row_begin) * H2, static_cast<uint32_t>(rows * H2 * 2));
+#pragma unroll
+      for (int it = 0; it < PIT; ++it) {
+        const int idx = it * kThreads + tid;
+        const uint32_t off = static_cast<uint32_t>(((idx / CH) * H2 + n0 + (idx % CH) * 8) * 2);
+        pre_g[it] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0));
+        pre_u[it] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ru, off + p.H * 2, 0, 0));
+      }
+      asm volatile("" ::: "memory");
+    }
+  };
   const int nks = k1 - k0;
   if (nks > 0) {
 #pragma unroll
@@ -977,6 +1001,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       interleave(kPart);
       cur = nxt;
     }
+    prefetch_up();
     ready(fa0, fb0);
     read_ks(cur, 1, fa1, fb1);
     mfma_ks(fa0, fb0);
@@ -988,8 +1013,18 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
     mfma_ks(fa0, fb0);
     ready(fa1, fb1);
     mfma_ks(fa1, fb1);
+  } else {
+    prefetch_up();
   }
-  wait_vmcnt_le(0);
+  if constexpr (EPI == EPI_GLU_BWD) {
+    // the stage loads (and their LDS writes) done; the 2 * PIT pre-activation
+    // loads issued after them may still be in flight
+    constexpr int kUp = 2 * PIT;
+    static_assert(kUp < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((kUp & 15) | ((kUp >> 4) << 14) | 0x70 | 0xF00);
+  } else {
+    wait_vmcnt_le(0);
+  }
   __syncthreads();
 
   if (role == ROLE_SPLIT) {
@@ -1117,10 +1152,6 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       }
     }
   };
-  // the GLU backward's pre-activation loads fly while the tile is staged
-  constexpr int PIT = (EPI == EPI_GLU_BWD) ? glu_bwd_items<BM, BN>() : 1;
-  uint4 pre_g[PIT], pre_u[PIT];
-  if constexpr (EPI == EPI_GLU_BWD) glu_bwd_prefetch<BM, BN>(p, row_begin, row_end, n0, pre_g, pre_u);
   if (role == ROLE_CUT && partner >= 0) stage(std::true_type{});
   else stage(std::false_type{});
   __syncthreads();
