@@ -56,8 +56,9 @@ STEP_KERNELS = {
     "ffmoe_route_fwd_ex": ["route_fwd"],
     "ffmoe_route_scan": ["route_scan"],
     "ffmoe_permute": ["permute"],
-    "ffmoe_gemm_up_glu": ["gemm_up_glu"],
-    "ffmoe_gemm_down": ["gemm_down"],
+    # up + GLU and down: one persistent launch (C2), or the two GEMMs where
+    # the fused schedule does not apply (timed together then)
+    "ffmoe_gemm_up_down": ["gemm_up_down"],
     "ffmoe_combine": ["combine", "dx_combine"],  # E > 32: the backward's dX gather is a combine
     "ffmoe_gate_logits": ["gate_logits"],
     "ffmoe_gate_dx": ["gate_dx"],
@@ -112,7 +113,7 @@ def algorithmic_work(c, rows):
     up_f = 2.0 * rows * D * 2 * H
     dn_f = 2.0 * rows * H * D
     return {
-        "gemm_up_glu": (up_f, "flop"), "gemm_down": (dn_f, "flop"),
+        "gemm_up_glu": (up_f, "flop"), "gemm_down": (dn_f, "flop"), "gemm_up_down": (up_f + dn_f, "flop"),
         "gemm_dgrad_glu": (dn_f, "flop"), "gemm_dgrad": (up_f, "flop"),
         "gemm_wgrad_down": (dn_f, "flop"), "gemm_wgrad_up": (up_f, "flop"),
         # x, gate read once; idx (8) + w (4) per entry and the bf16 logits written
@@ -249,10 +250,8 @@ def kernel_launches(c, x, gate, wu, wd, go):
            gws, st)
     L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), tr, E, T, H, D, P(ghb), gws, st)
     fns = {
-        "gemm_up_glu": lambda: L.call("ffmoe_gemm_up_glu", P(xs), P(wu), P(off), P(til), tr, E, T, D,
-                                      H, 0, P(up), P(act), gws, st),
-        "gemm_down": lambda: L.call("ffmoe_gemm_down", P(act), P(wd), P(off), P(til), tr, E, T, H, D,
-                                    P(down), gws, st),
+        "gemm_up_down": lambda: L.call("ffmoe_gemm_up_down_shared", P(xs), P(wu), P(wd), P(off), P(til), tr,
+                                       E, T, D, H, 0, P(up), P(act), P(down), None, None, gws, st),
         "gemm_dgrad_glu": lambda: L.call("ffmoe_gemm_dgrad_glu", P(wgo), P(wd), P(up), P(off), P(til),
                                          tr, E, T, D, H, 0, P(gup), gws, st),
         "gemm_dgrad": lambda: L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), tr, E, T, H,
@@ -351,7 +350,7 @@ def cpu_baseline(c, sample_tokens, runs=7):
 
 
 # the order traffic_mode launches the hot kernels in (each twice, after a flush)
-TRAFFIC_ORDER = ["gemm_up_glu", "gemm_down", "gemm_dgrad_glu", "gemm_dgrad", "gemm_wgrad_down",
+TRAFFIC_ORDER = ["gemm_up_down", "gemm_dgrad_glu", "gemm_dgrad", "gemm_wgrad_down",
                  "gemm_wgrad_up", "route_fwd", "permute", "combine", "route_bwd", "dx_reduce",
                  "gate_grad"]
 CAL_KIB = 256 * 1024  # the calibration copy reads and writes 256 MiB
@@ -429,6 +428,9 @@ def algorithmic_bytes(c, rows):
     out = {
         "gemm_up_glu": rows * D * b + E * 2 * H * D * b + rows * 2 * H * b + rows * H * b,
         "gemm_down": rows * H * b + E * D * H * b + rows * D * b,
+        # the two above: act written once and read back once
+        "gemm_up_down": (rows * D * b + E * 2 * H * D * b + rows * 2 * H * b + rows * H * b
+                         + rows * H * b + E * D * H * b + rows * D * b),
         "gemm_dgrad_glu": rows * D * b + E * D * H * b + 2 * rows * 2 * H * b,
         "gemm_dgrad": rows * 2 * H * b + E * 2 * H * D * b + rows * D * b,
         "gemm_wgrad_down": rows * D * b + rows * H * b + E * D * H * b,
@@ -485,9 +487,12 @@ def traffic_summary(fetch_csv, write_csv, out_path, commands):
         f.write("\n".join(lines))
 
 
-# the grouped-GEMM dispatches of one fwd+bwd step, in launch order
-GEMM_STEP_ORDER = ["gemm_up_glu", "gemm_down", "gemm_wgrad_down", "gemm_dgrad_glu", "gemm_wgrad_up",
-                   "gemm_dgrad"]
+# the grouped-GEMM dispatches of one fwd+bwd step, in launch order: the
+# forward's up + down as one fused launch, or as two where that schedule
+# does not apply
+GEMM_STEP_ORDER = ["gemm_up_down", "gemm_wgrad_down", "gemm_dgrad_glu", "gemm_wgrad_up", "gemm_dgrad"]
+GEMM_STEP_ORDER_UNFUSED = ["gemm_up_glu", "gemm_down", "gemm_wgrad_down", "gemm_dgrad_glu",
+                           "gemm_wgrad_up", "gemm_dgrad"]
 
 
 def stats_summary(prof_dir, bench_log, out_path, title, command):
@@ -511,7 +516,10 @@ def stats_summary(prof_dir, bench_log, out_path, title, command):
     # the grouped GEMMs only (not the dense gate GEMMs or their split-K reduce)
     gemm = [r["Kernel_Name"] for r in trace
             if "ffmoe::gemm_" in r["Kernel_Name"] and "dense" not in r["Kernel_Name"]]
-    order = GEMM_STEP_ORDER[:2] if (line or {}).get("pass") == "fwd" else GEMM_STEP_ORDER
+    fused = bool(gemm) and "updown" in gemm[0]
+    order = GEMM_STEP_ORDER if fused else GEMM_STEP_ORDER_UNFUSED
+    if (line or {}).get("pass") == "fwd":
+        order = order[:1] if fused else order[:2]
     role_sym = dict(zip(order, gemm[:len(order)]))
     total = sum(float(r["TotalDurationNs"]) for r in stats)
     out = [f"# rocprofv3 kernel statistics: {title}", "",

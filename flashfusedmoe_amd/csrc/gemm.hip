@@ -34,6 +34,15 @@ constexpr int MN_PAD = 16;  // elements of padding per MN-contiguous LDS row
 
 enum Epi { EPI_STORE = 0, EPI_GLU_FWD = 1, EPI_GLU_BWD = 2 };
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// buffer-instruction cache policy: sc1, device scope (coherent across XCDs)
+constexpr int kDeviceScope = 16;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
 static int g_use_tr = 1;  // LDS transpose reads for MN-contiguous operands
 
 struct GemmArgs {
@@ -78,6 +87,8 @@ struct GemmArgs {
   // (counter flags[kPairKey + tile], fp32 partial in slot `tile`)
   int x_split;
   int x_chunk;
+  // fused up+down launch: claim counter, exit counter, per-row-tile counts
+  int* fused;
 };
 
 // Grouped K: groups of the extra dense group (two when its K is split).
@@ -283,7 +294,7 @@ __device__ __forceinline__ void glu_bwd_store(const GemmArgs& p, const bf16_t* C
 // pre-activation) or GLU backward (reads the pre-activation, writes its
 // gradient).  Rows are row_base + i (grouped rows, valid below row_end) or
 // m_base + i (wgrad, valid below M).
-template <int ROWS, int BN, int LDC, int MODE, int EPI>
+template <int ROWS, int BN, int LDC, int MODE, int EPI, bool CO_C = false>
 __device__ __forceinline__ void store_c_tile(const GemmArgs& p, const bf16_t* Cs, int e, int m_base,
                                              int row_base, int row_end, int n0, int a0) {
   const int tid = threadIdx.x;
@@ -292,6 +303,12 @@ __device__ __forceinline__ void store_c_tile(const GemmArgs& p, const bf16_t* Cs
     constexpr int IT = ROWS * CH / kThreads;
     static_assert((ROWS * CH) % kThreads == 0, "whole items");
     const int64_t H = p.H;
+    // CO_C: the activation rows are read by other blocks of the same launch
+    // (the fused up+down GEMM): device-scope buffer stores (written through
+    // to the level every XCD reads), rows past the group dropped by bounds
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(p.C + static_cast<int64_t>(row_base) * p.ldc,
+                  static_cast<uint32_t>(max(0, min(row_end - row_base, ROWS)) * p.ldc * 2));
     with_act(p.act, [&](auto actc) {
       constexpr int ACT = decltype(actc)::value;
 #pragma unroll 4
@@ -312,7 +329,11 @@ __device__ __forceinline__ void store_c_tile(const GemmArgs& p, const bf16_t* Cs
             *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + a) = gv;
             *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + H + a) = uv;
           }
-          *reinterpret_cast<uint4*>(p.C + row * p.ldc + a) = pack8(o);
+          if constexpr (CO_C)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, pack8(o)), rc,
+                                                   static_cast<uint32_t>((ml * p.ldc + a) * 2), 0, kDeviceScope);
+          else
+            *reinterpret_cast<uint4*>(p.C + row * p.ldc + a) = pack8(o);
         }
       }
     });
@@ -588,6 +609,13 @@ constexpr int DL_BK = 64;
 // of at most 384 rows + columns), else two.
 template <int BM, int BN>
 constexpr int dl_stages() { return (BM + BN) <= 384 ? 3 : 2; }
+// LDS elements of a tile: the stage ring, or the C staging tile (rows of
+// BN + 8) the epilogue reuses it for, whichever is larger.
+template <int BM, int BN>
+constexpr int dl_smem_elems() {
+  return dl_stages<BM, BN>() * (BM + BN) * 64 > BM * (BN + 8) ? dl_stages<BM, BN>() * (BM + BN) * 64
+                                                               : BM * (BN + 8);
+}
 
 __device__ __forceinline__ void wait_vmcnt_le(int n) {
   // s_waitcnt with only the vector-memory count constrained (expcnt and
@@ -616,12 +644,6 @@ constexpr int issue_parts() {
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                           static_cast<int>(bytes), 0x00020000);
-}
 
 // Which part of a tile's K range a block computes.  ROLE_FULL: all of it,
 // then the epilogue.  ROLE_CUT: one of the two K ranges of a tile cut
@@ -650,12 +672,10 @@ __device__ __forceinline__ int ld_const(const int32_t* p, int i) {
   return ((const const_i32_t*)p)[i];
 }
 
-// Grouped-rows tile t of a grid of m_count row tiles x n_tiles column tiles.
+// Grouped-rows tile of row tile mt and column tile nt.
 template <int BM, int BN>
-__device__ __forceinline__ TileCoord decode_rows_tile(const GemmArgs& p, int64_t t, int m_count) {
+__device__ __forceinline__ TileCoord decode_rows_mn(const GemmArgs& p, int mt, int nt) {
   TileCoord c{};
-  int mt, nt;
-  grouped_order(t, m_count, p.n_tiles, &mt, &nt);
   c.n0 = nt * BN;
   const int R = ld_const(p.tile_offsets, p.E);
   c.valid = mt < R + extra_tiles<BM>(p);
@@ -676,6 +696,14 @@ __device__ __forceinline__ TileCoord decode_rows_tile(const GemmArgs& p, int64_t
   c.row_begin = ld_const(p.offsets, lo) + (mt - ld_const(p.tile_offsets, lo)) * BM;
   c.row_end = ld_const(p.offsets, lo + 1);
   return c;
+}
+
+// Grouped-rows tile t of a grid of m_count row tiles x n_tiles column tiles.
+template <int BM, int BN>
+__device__ __forceinline__ TileCoord decode_rows_tile(const GemmArgs& p, int64_t t, int m_count) {
+  int mt, nt;
+  grouped_order(t, m_count, p.n_tiles, &mt, &nt);
+  return decode_rows_mn<BM, BN>(p, mt, nt);
 }
 
 // Grouped-K (wgrad) tile t: expert-major, then grouped over M x N tiles.
@@ -704,15 +732,24 @@ __device__ __forceinline__ TileCoord decode_k_tile(const GemmArgs& p, int64_t t)
 }
 
 constexpr int kSpinLimit = 1 << 22;  // flag polls before a wait gives up
-// buffer-instruction cache policy: sc1, device scope (coherent across XCDs)
-constexpr int kDeviceScope = 16;
 
 // One tile (K steps [k0, k1); k1 < 0: to the end of K).  The body is a
 // __device__ function (the buffer-descriptor type exists only in the device
 // pass); the kernels below loop over tiles with it.
-template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
+// CO (fused up+down launch): kCoLoadA = the A rows were written by other
+// blocks of this launch (device-scope loads), kCoStoreC = the C rows are
+// read by other blocks of this launch (device-scope stores; the caller
+// counts them complete through the next tile's signal).  XS: the LDS buffer is the caller's (xsm), so that one
+// kernel can run tiles of two shapes out of one allocation.
+constexpr int kCoLoadA = 1, kCoStoreC = 2;
+// signal (fused up+down launch): a counter thread 0 adds 1 to once every
+// thread has waited for all its earlier vector-memory operations (vmcnt 0)
+// and a block barrier has followed, i.e. once the previous tile's stores are
+// complete; with two stages that is the first K step's wait.
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI, int CO = 0, bool XS = false>
 __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord& tc, int k0, int k1,
-                                             int role, int slot, int key) {
+                                             int role, int slot, int key, bf16_t* xsm = nullptr,
+                                             int* signal = nullptr) {
   // a tile of the extra dense group reads and writes its own tensors
   GemmArgs p = pa;
   if (tc.extra) {
@@ -733,11 +770,13 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   constexpr int LB = BN * DL_BK / 8 / kThreads;
   constexpr int LDC = BN + 8;                // C staging row stride
   constexpr int NS = dl_stages<BM, BN>();
-  constexpr int SMEM = (NS * STAGE > BM * LDC) ? NS * STAGE : BM * LDC;
+  constexpr int SMEM = dl_smem_elems<BM, BN>();
+  static_assert(SMEM == ((NS * STAGE > BM * LDC) ? NS * STAGE : BM * LDC), "LDS size");
   static_assert(SMEM * 2 <= 160 * 1024, "LDS budget");
   constexpr int NF = TM * TN * 4;            // fp32 partial: float4s per thread
   static_assert(EPI != EPI_GLU_FWD || (TN % 2 == 0), "GLU forward pairs gate/up tiles");
-  __shared__ __attribute__((aligned(1024))) bf16_t smem[SMEM];
+  __shared__ __attribute__((aligned(1024))) bf16_t smem_own[XS ? 1 : SMEM];
+  bf16_t* const smem = XS ? xsm : smem_own;
 
   // tile coordinates are block-uniform; readfirstlane keeps them (and the
   // buffer descriptors built from them) in scalar registers even where the
@@ -827,7 +866,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
     for (int i = part * PA; i < (part + 1) * PA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           ra, (lds_void_t*)(at + (i * kThreads + wave * 64) * 8), 16,
-          live ? offa[i] + kstep * stepa : 0xFFFFFFF0u, 0, 0, 0);
+          live ? offa[i] + kstep * stepa : 0xFFFFFFF0u, 0, 0, (CO & kCoLoadA) ? kDeviceScope : 0);
 #pragma unroll
     for (int i = part * PB; i < (part + 1) * PB; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -997,6 +1036,10 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
+      if constexpr (kIn == 0) {
+        if (i == 0 && signal != nullptr && tid == 0)
+          __hip_atomic_fetch_add(signal, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       // refill this stage's buffer NS steps ahead (part 0 now, the rest with
       // the next k-steps), read k-step 0 of the next stage, run k-step 3 of
       // this one
@@ -1034,6 +1077,8 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
     wait_vmcnt_le(0);
   }
   __syncthreads();
+  if (signal != nullptr && (kIn != 0 || nks < 2) && tid == 0)
+    __hip_atomic_fetch_add(signal, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   if (role == ROLE_SPLIT) {
     // row r of the tile holds output row row_begin + r (grouped rows) or
@@ -1166,7 +1211,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   if constexpr (EPI == EPI_GLU_BWD)
     glu_bwd_store<BM, BN, LDC>(p, Cs, row_begin, row_end, n0, pre_g, pre_u);
   else
-    store_c_tile<BM, BN, LDC, MODE, EPI>(p, Cs, e, m0, row_begin, row_end, n0, a0);
+    store_c_tile<BM, BN, LDC, MODE, EPI, (CO & kCoStoreC) != 0>(p, Cs, e, m0, row_begin, row_end, n0, a0);
   __syncthreads();  // the C tile is read before a next tile's loads refill the LDS
 }
 
@@ -1262,6 +1307,157 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
     gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_CUT, tc.xt, kPairKey + tc.xt);
   else
     gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
+#endif
+}
+
+// Fused up+down launch: the up GEMM with its GLU epilogue and the down GEMM
+// in one persistent grid (G blocks, a multiple of 8), so the down tiles of
+// finished row tiles fill the up GEMM's last, partial round.  Words of
+// p.fused (zero on entry; the last block out zeroes them again):
+//   [0, 8)                   up-tile claim counters of the 8 XCD slots
+//   kFusedDown               down-tile claim counter
+//   kFusedExit               blocks that have left
+//   [kFusedRow0, + R)        finished up tiles of each row tile
+// Up tiles, in grouped order, are cut into chunks of S = G / 8; chunk c
+// belongs to slot c % 8, so in round k each XCD runs one chunk and the
+// chunks start in tile order.  A block claims up tiles from its own slot
+// (blockIdx % 8: the XCD it is dispatched to), then from any slot that still
+// has some, and only then claims down tiles (row-major, the order the row
+// tiles finish in).  A down tile waits until all up tiles of its row tile
+// are counted; by then every up tile has been claimed by a running block and
+// up tiles wait for nothing, so the wait ends without any co-residency
+// guarantee (it is bounded all the same: a timeout sets the error word).
+// Each claim for the next tile is issued before the current tile, so its
+// latency hides under the tile (it is the oldest vector-memory operation of
+// the tile's waves, which only makes the tile's counted waits stricter).  The act rows cross blocks (and XCDs):
+// up tiles store them with device-scope stores completed before the row
+// count moves, down tiles load them with device-scope loads.
+constexpr int kFusedDown = 8, kFusedExit = 9, kFusedRow0 = 16;
+constexpr int kFusedWords = 16384;
+constexpr int64_t kFusedBytes = kFusedWords * 4;
+
+template <int BM>
+__global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, GemmArgs pd) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
+  constexpr int BNU = 256, BND = 128;
+  constexpr int SU = dl_smem_elems<BM, BNU>(), SD = dl_smem_elems<BM, BND>();
+  // One LDS variable: with a second one the compiler scopes the
+  // direct-to-LDS loads by variable and then waits for all of them (vmcnt 0)
+  // before LDS reads in the K loops.  The claim words follow the tiles' area.
+  constexpr int SMAX = SU > SD ? SU : SD;
+  __shared__ __attribute__((aligned(1024))) bf16_t sm[SMAX + 8];
+  int* const s_word = reinterpret_cast<int*>(sm + SMAX);
+  int* const fl = pu.fused;
+  const int tid = threadIdx.x;
+  const int R = ld_const(pu.tile_offsets, pu.E) + extra_tiles<BM>(pu);
+  const int NU = pu.n_tiles, ND = pd.n_tiles;
+  const int64_t TU = static_cast<int64_t>(R) * NU, TD = static_cast<int64_t>(R) * ND;
+  const int S = static_cast<int>(gridDim.x >> 3);
+  // up tile of claim j of slot x (>= TU once the slot is empty)
+  auto up_tile = [&](int j, int x) { return (static_cast<int64_t>(j / S) * 8 + x) * S + j % S; };
+  auto fetch_add = [&](int w) { return __hip_atomic_fetch_add(fl + w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  // The claim of the next tile: one atomic add, from lane 0 of wave 0 (the
+  // other waves run the instruction with no lane on), returning into that
+  // lane with no wait.  It is written in assembly because compiled code
+  // waits for the value where a one-lane branch rejoins; thread 0 reads it
+  // only after a vmcnt(0) wait at the end of the tile.
+  auto claim_ahead = [&](int w) {
+    int v;
+    uint64_t save;
+    const int lanes = __builtin_amdgcn_readfirstlane(threadIdx.x < 64 ? 1 : 0);
+    asm volatile(
+        "s_mov_b64 %1, exec\n\t"
+        "s_mov_b32 exec_lo, %4\n\t"
+        "s_mov_b32 exec_hi, 0\n\t"
+        "global_atomic_add %0, %2, %3, off sc0\n\t"
+        "s_mov_b64 exec, %1"
+        : "=&v"(v), "=&s"(save)
+        : "v"(fl + w), "v"(1), "s"(lanes)
+        : "memory");
+    return v;
+  };
+  // one claim, broadcast to the block
+  auto claim = [&](int w) {
+    if (tid == 0) s_word[0] = fetch_add(w);
+    __syncthreads();
+    const int v = s_word[0];
+    __syncthreads();
+    return v;
+  };
+  const int home = static_cast<int>(blockIdx.x & 7);
+  int x = home;
+  int prev_row = -1;  // row tile of this block's last up tile, not yet counted
+  int j = claim(x);
+  for (;;) {
+    const int64_t t = up_tile(j, x);
+    if (t >= TU) {
+      // this slot is empty: move to the next one (from the home slot on)
+      // that is not
+      if (tid < 64) {
+        const int c = tid < 8 ? __hip_atomic_load(fl + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        const uint32_t m = static_cast<uint32_t>(__ballot(tid < 8 && up_tile(c, tid) < TU)) & 0xFFu;
+        if (tid == 0) {
+          const uint32_t rot = ((m >> (home + 1)) | (m << (7 - home))) & 0xFFu;  // bit i: slot home + 1 + i
+          s_word[1] = rot ? (home + 1 + __builtin_ctz(rot)) & 7 : -1;
+        }
+      }
+      __syncthreads();
+      const int ns = s_word[1];
+      __syncthreads();
+      if (ns < 0) break;
+      x = ns;
+      j = claim(x);
+      continue;
+    }
+    const int nj = claim_ahead(x);
+    int mt, nt;
+    grouped_order(t, R, NU, &mt, &nt);
+    const TileCoord tc = decode_rows_mn<BM, BNU>(pu, mt, nt);
+    // counts the previous up tile of this block done once its act stores
+    // are (during the K loop); it waits for all vector-memory operations
+    // (the claim's too) before its epilogue
+    gemm_dl_tile<BM, BNU, true, true, 0, EPI_GLU_FWD, kCoStoreC, true>(
+        pu, tc, 0, -1, ROLE_FULL, 0, 0, sm, prev_row >= 0 ? fl + kFusedRow0 + prev_row : nullptr);
+    prev_row = mt;
+    if (tid == 0) s_word[0] = nj;
+    __syncthreads();
+    j = s_word[0];
+    __syncthreads();
+  }
+  // the last up tile's act stores
+  wait_vmcnt_le(0);
+  __syncthreads();
+  if (prev_row >= 0 && tid == 0)
+    __hip_atomic_fetch_add(fl + kFusedRow0 + prev_row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int d = claim(kFusedDown);
+  while (d < TD) {
+    const int r = static_cast<int>(d / ND), c = static_cast<int>(d - static_cast<int64_t>(r) * ND);
+    if (tid == 0) {
+      int polls = 0;
+      while (__hip_atomic_load(fl + kFusedRow0 + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < NU) {
+        if (++polls >= kSpinLimit) {  // never expected: the tile is computed from whatever act holds
+          __hip_atomic_store(pu.flags + pu.err_idx, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    __syncthreads();
+    const int nd = claim_ahead(kFusedDown);  // after the wait's loads, which it would join
+    const TileCoord tc = decode_rows_mn<BM, BND>(pd, r, c);
+    gemm_dl_tile<BM, BND, true, true, 0, EPI_STORE, kCoLoadA, true>(pd, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+    if (tid == 0) s_word[0] = nd;  // the tile waited for all vector-memory operations before its epilogue
+    __syncthreads();
+    d = s_word[0];
+    __syncthreads();
+  }
+  // the last block out has seen every block finish all its tiles: it clears
+  // the words for the next launch
+  if (tid == 0) s_word[1] = fetch_add(kFusedExit);
+  __syncthreads();
+  if (s_word[1] == static_cast<int>(gridDim.x) - 1)
+    for (int i = tid; i < kFusedRow0 + R; i += kThreads)
+      __hip_atomic_store(fl + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #endif
 }
 
@@ -1510,9 +1706,13 @@ extern "C" int ffmoe_gemm_tile_rows(int64_t max_rows, int E) {
   return (E > 0 && max_rows / E >= 384) ? 256 : 128;
 }
 
+// Workspace: the persistent GEMMs' flag words, their fp32 partial slots (two
+// per block), then the fused up+down launch's words.
+static int64_t fused_words_offset(int G) { return kSkFlagBytes + 2 * static_cast<int64_t>(G) * kSkSlotBytes; }
+
 extern "C" int64_t ffmoe_gemm_workspace_bytes(void) {
   const int G = sk_blocks();
-  return G > 0 ? kSkFlagBytes + 2 * static_cast<int64_t>(G) * kSkSlotBytes : -1;
+  return G > 0 ? fused_words_offset(G) + kFusedBytes : -1;
 }
 
 extern "C" int ffmoe_gemm_check(void* sk_workspace, void* stream) {
@@ -1529,7 +1729,9 @@ extern "C" int ffmoe_gemm_check(void* sk_workspace, void* stream) {
   if (err == 0) return clear_error();
   // every block of the failed launch has finished (the stream is idle), so
   // clearing the flag words here cannot race a late publication
-  if (hipMemsetAsync(sk_workspace, 0, kSkFlagBytes, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+  if (hipMemsetAsync(sk_workspace, 0, kSkFlagBytes, st) != hipSuccess ||
+      hipMemsetAsync(static_cast<char*>(sk_workspace) + fused_words_offset(G), 0, kFusedBytes, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
     return set_error("ffmoe_gemm_check: cannot clear the workspace");
   return set_error(
       "ffmoe_gemm_check: a stream-K partner wait timed out in an earlier grouped GEMM on this workspace; "
@@ -1603,6 +1805,65 @@ extern "C" int ffmoe_gemm_down(const void* act, const void* w_down, const int32_
                                int H, int D, void* down_out, void* sk_workspace, void* stream) {
   return ffmoe_gemm_down_shared(act, w_down, offsets, tile_offsets, tile_rows, E, max_rows, H, D, down_out,
                                 nullptr, sk_workspace, stream);
+}
+
+// The up GEMM + GLU and the down GEMM in one persistent launch where that
+// schedule applies (256-row tiles, K of both a multiple of 64, the up GEMM's
+// K below the stream-K threshold, a workspace), else the two launches.
+extern "C" int ffmoe_gemm_up_down_shared(const void* x_sorted, const void* w_up, const void* w_down,
+                                         const int32_t* offsets, const int32_t* tile_offsets, int tile_rows,
+                                         int E, int64_t max_rows, int D, int H, int activation, void* up_out,
+                                         void* act_out, void* down_out, const ffmoe_dense_group* shared_up,
+                                         const ffmoe_dense_group* shared_down, void* sk_workspace,
+                                         void* stream) {
+  if (check_rows("ffmoe_gemm_up_down", E, max_rows, D, H, tile_rows)) return 1;
+  if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_gemm_up_down: unknown activation");
+  const bool su = shared_up != nullptr && shared_up->rows > 0, sd = shared_down != nullptr && shared_down->rows > 0;
+  if (su != sd || (su && (shared_up->rows != shared_down->rows || shared_down->a != shared_up->c)))
+    return set_error("ffmoe_gemm_up_down: the dense group's down GEMM must read its up GEMM's activation rows");
+  const int G = sk_blocks() / 8 * 8;
+  const int64_t row_tiles = (max_rows + tile_rows - 1) / tile_rows + E + (su ? (shared_up->rows + tile_rows - 1) / tile_rows : 0);
+  const bool fused = sk_workspace != nullptr && g_use_tr && tile_rows == 256 && D % DL_BK == 0 && H % DL_BK == 0 &&
+                     D < kSkMinK && G >= 8 && row_tiles <= kFusedWords - kFusedRow0;
+  if (!fused) {
+    if (ffmoe_gemm_up_glu_shared(x_sorted, w_up, offsets, tile_offsets, tile_rows, E, max_rows, D, H, activation,
+                                 up_out, act_out, shared_up, sk_workspace, stream))
+      return 1;
+    return ffmoe_gemm_down_shared(act_out, w_down, offsets, tile_offsets, tile_rows, E, max_rows, H, D, down_out,
+                                  shared_down, sk_workspace, stream);
+  }
+  constexpr int BNU = 256, BND = 128;
+  GemmArgs u = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BNU / 2 - 1) / (BNU / 2));
+  u.A = static_cast<const bf16_t*>(x_sorted);
+  u.B = static_cast<const bf16_t*>(w_up);
+  u.C = static_cast<bf16_t*>(act_out);
+  u.C2 = static_cast<bf16_t*>(up_out);
+  u.lda = D;
+  u.ldb = D;
+  u.ldc = H;
+  u.b_stride = static_cast<int64_t>(2) * H * D;
+  u.N = H;
+  u.K = D;
+  u.H = H;
+  u.act = activation;
+  if (apply_shared(u, shared_up, tile_rows, "ffmoe_gemm_up_down")) return 1;
+  GemmArgs d = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BND - 1) / BND);
+  d.A = static_cast<const bf16_t*>(act_out);
+  d.B = static_cast<const bf16_t*>(w_down);
+  d.C = static_cast<bf16_t*>(down_out);
+  d.lda = H;
+  d.ldb = H;
+  d.ldc = D;
+  d.b_stride = static_cast<int64_t>(D) * H;
+  d.N = D;
+  d.K = H;
+  if (apply_shared(d, shared_down, tile_rows, "ffmoe_gemm_up_down")) return 1;
+  u.flags = static_cast<int*>(sk_workspace);
+  u.err_idx = 2 * sk_blocks();
+  u.fused = reinterpret_cast<int*>(static_cast<char*>(sk_workspace) + fused_words_offset(sk_blocks()));
+  hipLaunchKernelGGL(gemm_updown_kernel<256>, dim3(G), dim3(kThreads), 0, static_cast<hipStream_t>(stream), u, d);
+  if (check_launch("gemm_up_down")) return 1;
+  return clear_error();
 }
 
 extern "C" int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, const void* up,

@@ -276,10 +276,11 @@ def _up_down(xs, w_up, w_down, offsets, tile_offsets, activation, save_up, st, s
               torch.empty(N, D, dtype=_BF16, device=dev))
         g_up = L.dense_group(x, w_gu, sh[1], N, sact, c2=sh[0])
         g_down = L.dense_group(sh[1], w_sd, sh[2], N, 0)
-    L.call("ffmoe_gemm_up_glu_shared", L.ptr(xs), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr,
-           E, T, D, H, activation, L.ptr(up), L.ptr(act), _byref(g_up), ws, st)
-    L.call("ffmoe_gemm_down_shared", L.ptr(act), L.ptr(w_down), L.ptr(offsets), L.ptr(tile_offsets), tr,
-           E, T, H, D, L.ptr(down), _byref(g_down), ws, st)
+    # one persistent launch where it applies (a row tile's down tiles start
+    # as soon as its up tiles are done), else the two GEMMs
+    L.call("ffmoe_gemm_up_down_shared", L.ptr(xs), L.ptr(w_up), L.ptr(w_down), L.ptr(offsets),
+           L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(up), L.ptr(act), L.ptr(down),
+           _byref(g_up), _byref(g_down), ws, st)
     return up, act, down, sh
 
 

@@ -175,9 +175,10 @@ int ffmoe_permute(const void* x, const int64_t* topk_idx, float* topk_w,
 int ffmoe_gemm_tile_rows(int64_t max_rows, int E);
 
 /* Bytes of the `sk_workspace` the four grouped-rows GEMMs below take on the
- * current device (-1 if the device cannot be queried).  Its first 8 KiB are
- * int32 flags that must be zero before the first call; every call leaves them
- * zero again, so one workspace serves any number of calls in stream order.
+ * current device (-1 if the device cannot be queried).  Its first 8 KiB and
+ * its last 64 KiB are int32 flags that must be zero before the first call
+ * (allocate it zeroed); every call leaves them zero again, so one workspace
+ * serves any number of calls in stream order.
  * Calls that may overlap (different streams) need separate workspaces.
  * With sk_workspace NULL the GEMMs run one block per tile instead of the
  * persistent one-block-per-CU schedule whose last round is split along K.
@@ -215,6 +216,20 @@ int ffmoe_gemm_down_shared(const void* act, const void* w_down, const int32_t* o
                            const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
                            int H, int D, void* down_out, const ffmoe_dense_group* shared,
                            void* sk_workspace, void* stream);
+/* ffmoe_gemm_up_glu_shared followed by ffmoe_gemm_down_shared on its
+ * act_out (shared_down->a must be shared_up->c), as one persistent launch
+ * where it applies (tile_rows 256, D and H multiples of 64, D below 4096,
+ * sk_workspace given): a row tile's down tiles start as soon as all its up
+ * tiles are done, so they fill the up GEMM's last, partial round.  The
+ * outputs are those of the two calls (bit for bit those of the two calls
+ * with sk_workspace NULL: no tile's K range is split), which it makes
+ * itself where the fused schedule does not apply.  Replaces: the up bmm + activation and the
+ * down bmm (fused_moe.py:435-441). */
+int ffmoe_gemm_up_down_shared(const void* x_sorted, const void* w_up, const void* w_down,
+                              const int32_t* offsets, const int32_t* tile_offsets, int tile_rows,
+                              int E, int64_t max_rows, int D, int H, int activation, void* up_out,
+                              void* act_out, void* down_out, const ffmoe_dense_group* shared_up,
+                              const ffmoe_dense_group* shared_down, void* sk_workspace, void* stream);
 int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, const void* up,
                                 const int32_t* offsets, const int32_t* tile_offsets,
                                 int tile_rows, int E, int64_t max_rows, int D, int H,

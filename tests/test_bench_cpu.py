@@ -99,7 +99,7 @@ def test_traffic_summary_splits_dispatches_by_flush(tmp_path):
         t = bench.measured_traffic()
     finally:
         bench.TRAFFIC_FILE = orig
-    assert t["gemm_up_glu"] == int(round((101.0 * 2 + 101.0 * 2) * 1024))
+    assert t[bench.TRAFFIC_ORDER[0]] == int(round((101.0 * 2 + 101.0 * 2) * 1024))
 
 
 def test_algorithmic_bytes_of_the_gemms_at_c2():
@@ -107,6 +107,8 @@ def test_algorithmic_bytes_of_the_gemms_at_c2():
     a = bench.algorithmic_bytes(bench.CFG, 16384)
     MiB = 1 << 20
     assert a["gemm_up_glu"] == 288 * MiB     # xs 32 + w_up 64 + up 128 + act 64
+    assert a["gemm_down"] == 128 * MiB       # act 64 + w_down 32 + down 32
+    assert a["gemm_up_down"] == a["gemm_up_glu"] + a["gemm_down"]
     assert a["gemm_dgrad_glu"] == 320 * MiB  # wgo 32 + w_down 32 + up 128 + gup 128
     assert a["gemm_dgrad"] == 224 * MiB
     assert a["gemm_wgrad_down"] == 128 * MiB

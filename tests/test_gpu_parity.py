@@ -4,6 +4,8 @@ permutation) must be bit-exact; floating-point results must match within the
 bf16 tolerance of gpu_helpers.check_close (rtol 2e-2, atol 2e-3, fp32
 accumulation)."""
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -236,6 +238,71 @@ def test_persistent_schedule_is_deterministic(sizes, D, H, _lib):
         for a, b in zip(outs[0], run):
             assert torch.equal(a, b)
     assert int(wsb[:8192].view(torch.int32).abs().sum().item()) == 0
+
+
+# The fused up+down launch against the two separate launches (down with no
+# workspace: one block per tile, as in the fused schedule, so the outputs are
+# the same bits), with and without a dense group after the routed rows.
+# Cases with 128-row tiles take the two-launch path inside the entry point.
+@pytest.mark.parametrize("sizes,D,H,shared_rows", [
+    ([2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800], 1024, 2048, 0),
+    ([2048] * 8, 1024, 2048, 8192),
+    ([0, 1500, 0, 600], 256, 320, 0),
+    ([700, 900], 256, 64, 513),
+    ([300, 0, 128, 1, 513, 64, 0, 127], 256, 192, 0),
+])
+def test_fused_up_down_matches_two_launches(sizes, D, H, shared_rows, _lib):
+    L = _lib
+    E = len(sizes)
+    xs, wu, wd, off = _groups(E, sizes, D, H, seed=31 + sum(sizes))
+    T = xs.shape[0]
+    bm = L.gemm_tile_rows(T, E)
+    print(f"fused up+down: sizes={sizes} D={D} H={H} shared={shared_rows} tile_rows={bm}", flush=True)
+    tiles = np.zeros(E + 1, dtype=np.int32)
+    tiles[1:] = np.cumsum([-(-s // bm) for s in sizes])
+    xs_g, wu_g, wd_g = cuda(xs, wu, wd)
+    off_g = torch.from_numpy(off).cuda()
+    til_g = torch.from_numpy(tiles).cuda()
+    st = L.stream_ptr()
+    wsb = L.gemm_workspace(torch.device("cuda"), st)
+    g = torch.Generator().manual_seed(9)
+    N = shared_rows
+    sx = torch.randn(N, D, generator=g).to(torch.bfloat16).cuda()
+    sgu = (torch.randn(2 * H, D, generator=g) * D ** -0.5).to(torch.bfloat16).cuda()
+    sdn = (torch.randn(D, H, generator=g) * H ** -0.5).to(torch.bfloat16).cuda()
+
+    def outputs():
+        bf = dict(dtype=torch.bfloat16, device="cuda")
+        o = [torch.empty(T, 2 * H, **bf), torch.empty(T, H, **bf), torch.empty(T, D, **bf),
+             torch.empty(N, 2 * H, **bf), torch.empty(N, H, **bf), torch.empty(N, D, **bf)]
+        gu = L.dense_group(sx, sgu, o[4], N, 0, c2=o[3]) if N else None
+        gd = L.dense_group(o[4], sdn, o[5], N, 0) if N else None
+        return o, (ctypes.byref(gu) if gu else None), (ctypes.byref(gd) if gd else None)
+
+    ref, gu, gd = outputs()
+    L.call("ffmoe_gemm_up_glu_shared", xs_g.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
+           bm, E, T, D, H, 0, ref[0].data_ptr(), ref[1].data_ptr(), gu, None, st)
+    L.call("ffmoe_gemm_down_shared", ref[1].data_ptr(), wd_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
+           bm, E, T, H, D, ref[2].data_ptr(), gd, None, st)
+    for _ in range(3):
+        got, gu, gd = outputs()
+        L.call("ffmoe_gemm_up_down_shared", xs_g.data_ptr(), wu_g.data_ptr(), wd_g.data_ptr(), off_g.data_ptr(),
+               til_g.data_ptr(), bm, E, T, D, H, 0, got[0].data_ptr(), got[1].data_ptr(), got[2].data_ptr(),
+               gu, gd, wsb.data_ptr(), st)
+        torch.cuda.synchronize()
+        for name, a, b in zip(["up", "act", "down", "shared up", "shared act", "shared down"], got, ref):
+            assert torch.equal(a, b), name
+    # the schedule's words are left zero and no wait timed out
+    assert int(wsb[:8192].view(torch.int32).abs().sum().item()) == 0
+    assert int(wsb[-65536:].view(torch.int32).abs().sum().item()) == 0
+    # and the result is the product: the routed rows against fp32
+    f = lambda t: t.float()  # noqa: E731
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b > a:
+            check_close(ref[2][a:b], f(ref[1][a:b]) @ f(wd_g[e]).t(), f"down[e={e}]")
+    if N:
+        check_close(ref[5], f(ref[4]) @ f(sdn).t(), "shared down")
 
 
 @pytest.mark.parametrize("E", [3, 8, 32])
