@@ -176,8 +176,18 @@ __device__ __forceinline__ void unpack4(uint2 v, float* f) {
   f[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
+// Chunk swizzle of k-row k of an MN-contiguous stage tile of R columns:
+// 16-byte chunk c sits at chunk c ^ mn_swz<R>(k).  Rows of 128 columns or
+// more: (k & 3) << 2 (four rows cover distinct bank slots); rows of 64
+// (128 bytes, so rows k and k + 2 share banks): ((k >> 1) & 1) << 2.  Both
+// are the same for rows k and k + 4.
+template <int R>
+__device__ __forceinline__ constexpr int mn_swz(int k) {
+  return R >= 128 ? (k & 3) << 2 : ((k >> 1) & 1) << 2;
+}
+
 // Transpose-read fragment from a swizzled MN-contiguous stage tile [32][R]
-// whose 16-byte chunk c of k-row k sits at chunk c ^ ((k & 3) << 2).
+// (chunk swizzle mn_swz<R>).
 //
 // The two ds_read_b64_tr_b16 are issued as inline assembly: after a
 // direct-to-LDS buffer load the compiler conservatively puts a vmcnt(0) wait
@@ -191,7 +201,7 @@ __device__ __forceinline__ bf16x8_t lds_frag_mn_sw(const bf16_t* t, int c0, int 
   const int g = lane >> 4, i = lane & 15;
   const int kb = ks * 16 + (g >> 1) * 8 + (i >> 2);
   const int col = c0 + (g & 1) * 16 + (i & 3) * 4;
-  const int sw = (kb & 3) << 2;  // same for rows kb and kb + 4
+  const int sw = mn_swz<R>(kb);  // same for rows kb and kb + 4
   const int off = (((col >> 3) ^ sw) << 3) + (col & 7);
   const uint32_t a0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(t + kb * R + off));
   typedef unsigned int u32x2v_t __attribute__((ext_vector_type(2)));
@@ -598,7 +608,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 //     chunk c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128 cycle serves hit
 //     16 distinct 16-byte bank slots (64 banks x 4 bytes).
 //   MN-contiguous stage tile [64][R]: chunk c of k-row k stored at
-//     c ^ ((k & 3) << 2): the 2 x 4 rows x 32 bytes of one transpose-read
+//     c ^ mn_swz<R>(k): the 2 x 4 rows x 32 bytes of one transpose-read
 //     cycle hit distinct bank slots.
 // Each 64-K stage is four MFMA k-steps of 16; operand fragments are
 // double-buffered in registers.  Before the last k-step of stage kt: wait for
@@ -606,9 +616,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 // kt+NS, read stage kt+1's first fragments, then run the last k-step.
 constexpr int DL_BK = 64;
 // Stages of the LDS ring: three where they fit in the 160 KiB of LDS (tiles
-// of at most 384 rows + columns), else two.
+// of at most 384 rows + columns), else two; two for the 64-column tiles,
+// which run two blocks per CU (80 KiB each).
 template <int BM, int BN>
-constexpr int dl_stages() { return (BM + BN) <= 384 ? 3 : 2; }
+constexpr int dl_stages() { return BN == 64 ? 2 : ((BM + BN) <= 384 ? 3 : 2); }
 // LDS elements of a tile: the stage ring, or the C staging tile (rows of
 // BN + 8) the epilogue reuses it for, whichever is larger.
 template <int BM, int BN>
@@ -821,7 +832,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       const int r = pos >> 3, c = (pos & 7) ^ ((r >> 1) & 7);
       offa[i] = static_cast<uint32_t>((r * p.lda + c * 8) * 2);
     } else {
-      const int k = pos / (BM / 8), c = (pos % (BM / 8)) ^ ((k & 3) << 2);
+      const int k = pos / (BM / 8), c = (pos % (BM / 8)) ^ mn_swz<BM>(k);
       offa[i] = static_cast<uint32_t>((k * p.lda + m0 + c * 8) * 2);
     }
   }
@@ -839,7 +850,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       }
       offb[i] = static_cast<uint32_t>((static_cast<int64_t>(brow) * p.ldb + c * 8) * 2);
     } else {
-      const int k = pos / (BN / 8), c = (pos % (BN / 8)) ^ ((k & 3) << 2);
+      const int k = pos / (BN / 8), c = (pos % (BN / 8)) ^ mn_swz<BN>(k);
       offb[i] = static_cast<uint32_t>((k * p.ldb + n0 + c * 8) * 2);
     }
   }
@@ -1224,9 +1235,9 @@ constexpr int kPairKey = 1024;
 constexpr int kPairPubOff = 512;
 constexpr int kPairMax = 512;
 
-// One block per tile.
+// Body of the one-block-per-tile kernels.
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
-__global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
+__device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   TileCoord tc;
   if constexpr (MODE == 0) {
     // Blocks are dispatched round-robin over the 8 XCDs (XCD x runs blocks
@@ -1309,6 +1320,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
     gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
 #endif
 }
+
+// One block per tile.
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
+  gemm_dl_body<BM, BN, A_KC, B_KC, MODE, EPI>(p);
+}
+
+// The same, two blocks per CU (at most 256 registers a lane, 80 KiB of
+// LDS): one block's epilogue runs beside the other's K loop.  Grouped rows.
+template <int BM, int BN, bool A_KC, bool B_KC, int EPI>
+__global__ __launch_bounds__(kThreads, 2) void gemm_dl2_kernel(GemmArgs p) {
+  gemm_dl_body<BM, BN, A_KC, B_KC, 0, EPI>(p);
+}
+
 
 // Fused up+down launch: the up GEMM with its GLU epilogue and the down GEMM
 // in one persistent grid (G blocks, a multiple of 8), so the down tiles of
@@ -1873,7 +1898,12 @@ extern "C" int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, 
                                            void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
-  constexpr int BN = 128;  // 256 x 128 tiles: a three-stage LDS ring fits
+  // 256-row tiles: 256 x 64 tiles two blocks per CU, so one block's GLU
+  // backward epilogue (VALU work: about a third of a tile) overlaps the
+  // other's K loop (C2: 142 -> 122 us, measured); else 256 x 128 (or
+  // 128 x 128) tiles, a three-stage LDS ring, one block per CU
+  const bool two_per_cu = tile_rows == 256 && g_use_tr && D % DL_BK == 0;
+  const int BN = two_per_cu ? 64 : 128;
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(wgo);
   a.B = static_cast<const bf16_t*>(w_down);
@@ -1890,8 +1920,17 @@ extern "C" int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, 
   if (shared != nullptr && shared->rows > 0 && shared->up == nullptr)
     return set_error("ffmoe_gemm_dgrad_glu: the dense extra group needs its pre-activation");
   if (apply_shared(a, shared, tile_rows, "ffmoe_gemm_dgrad_glu")) return 1;
-  return launch_rows<BN, false, EPI_GLU_BWD>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
-                                             "gemm_dgrad_glu");
+  if (two_per_cu) {
+    if (a.total_tiles <= 0) return clear_error();
+    const int64_t grid = (a.total_tiles + 7) / 8 * 8;
+    if (grid > 0x7fffffff) return set_error("ffmoe_gemm_dgrad_glu: problem too large");
+    hipLaunchKernelGGL((gemm_dl2_kernel<256, 64, true, false, EPI_GLU_BWD>), dim3(static_cast<unsigned>(grid)),
+                       dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+    if (check_launch("gemm_dgrad_glu")) return 1;
+    return clear_error();
+  }
+  return launch_rows<128, false, EPI_GLU_BWD>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
+                                              "gemm_dgrad_glu");
 }
 
 extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const void* up,

@@ -135,6 +135,8 @@ def _groups(E, sizes, D, H, seed):
     ([2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800], 1024, 2048),
     ([2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800], 4096, 512),
     ([5, 17, 0, 260], 96, 40),
+    # 256-row tiles with H not a multiple of the 64-column dgrad+GLU tiles
+    ([700, 0, 900], 256, 200),
 ])
 @pytest.mark.parametrize("mode", ["sk", "dp", "elementwise"])
 def test_grouped_gemms_against_fp32(sizes, D, H, mode, _lib):
