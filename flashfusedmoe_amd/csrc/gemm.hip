@@ -1638,6 +1638,7 @@ static int launch(const GemmArgs& a, hipStream_t st, const char* name) {
 // Persistent blocks per device: one per CU.
 constexpr int kMaxSkBlocks = 1023;
 constexpr int kSkMinK = 4096;
+constexpr int kSkMaxRounds = 8;
 constexpr int64_t kSkFlagBytes = 8192;  // int32 counters [G], publications [G], error word; zero on entry
 constexpr int64_t kSkSlotBytes = 256 * 256 * 4;  // fp32 partial of the largest tile
 
@@ -1664,6 +1665,11 @@ static int launch_sk(GemmArgs a, void* ws, int min_k, hipStream_t st, const char
     return launch<BM, BN, true, B_KC, 0, EPI>(a, st, name);
   const int G = sk_blocks();
   if (G <= 0) return set_error(std::string(name) + ": cannot query the CU count");
+  // at 8 or more rounds of tiles (the host's upper bound) the last round's
+  // quantisation is small and the cut tiles' partials cost more than they
+  // save: one block per tile (C5: dgrad 4.11 -> 3.75 ms, dgrad+GLU 2.25 ->
+  // 2.16 ms; C4: dgrad 1.49 -> 1.44 ms, dgrad+GLU 1.00 -> 0.95 ms)
+  if (a.total_tiles >= static_cast<int64_t>(kSkMaxRounds) * G) return launch<BM, BN, true, B_KC, 0, EPI>(a, st, name);
   a.flags = static_cast<int*>(ws);
   a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kSkFlagBytes);
   a.pub_off = G;
@@ -1898,11 +1904,13 @@ extern "C" int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, 
                                            void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
-  // 256-row tiles: 256 x 64 tiles two blocks per CU, so one block's GLU
-  // backward epilogue (VALU work: about a third of a tile) overlaps the
-  // other's K loop (C2: 142 -> 122 us, measured); else 256 x 128 (or
-  // 128 x 128) tiles, a three-stage LDS ring, one block per CU
-  const bool two_per_cu = tile_rows == 256 && g_use_tr && D % DL_BK == 0;
+  // 256-row tiles and a short K (= D): 256 x 64 tiles two blocks per CU,
+  // so one block's GLU backward epilogue (VALU work: about a third of a
+  // 256 x 128 tile at K = 1024) overlaps the other's K loop (C2, D 1024:
+  // 142 -> 122 us; C4, D 2048, where the epilogue is a smaller share:
+  // 1.01 -> 1.15 ms, so not there); else 256 x 128 (or 128 x 128) tiles,
+  // a three-stage LDS ring, one block per CU
+  const bool two_per_cu = tile_rows == 256 && g_use_tr && D % DL_BK == 0 && D <= 1024;
   const int BN = two_per_cu ? 64 : 128;
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(wgo);
