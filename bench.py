@@ -63,9 +63,11 @@ STEP_KERNELS = {
     "ffmoe_gate_logits": ["gate_logits"],
     "ffmoe_gate_dx": ["gate_dx"],
     "ffmoe_route_bwd_ex": ["route_bwd"],
-    "ffmoe_gemm_wgrad": ["gemm_wgrad_down", "gemm_wgrad_up"],
+    "ffmoe_gemm_wgrad": ["gemm_wgrad_down"],
     "ffmoe_gemm_dgrad_glu": ["gemm_dgrad_glu"],
-    "ffmoe_gemm_dgrad": ["gemm_dgrad"],
+    # dX's GEMM and the up-side weight gradient: one persistent launch, or
+    # the two GEMMs where the fused schedule does not apply (timed together)
+    "ffmoe_gemm_dgrad_wgrad": ["gemm_dgrad_wgrad"],
     "ffmoe_dx_reduce": ["dx_reduce"],
     "ffmoe_gate_grad": ["gate_grad"],
 }
@@ -116,6 +118,7 @@ def algorithmic_work(c, rows):
         "gemm_up_glu": (up_f, "flop"), "gemm_down": (dn_f, "flop"), "gemm_up_down": (up_f + dn_f, "flop"),
         "gemm_dgrad_glu": (dn_f, "flop"), "gemm_dgrad": (up_f, "flop"),
         "gemm_wgrad_down": (dn_f, "flop"), "gemm_wgrad_up": (up_f, "flop"),
+        "gemm_dgrad_wgrad": (2 * up_f, "flop"),
         # x, gate read once; idx (8) + w (4) per entry and the bf16 logits written
         "route_fwd": (N * D * b + E * D * b + T * 12 + N * E * b, "byte"),
         "route_scan": (None, "byte"),
@@ -254,12 +257,10 @@ def kernel_launches(c, x, gate, wu, wd, go):
                                        E, T, D, H, 0, P(up), P(act), P(down), None, None, gws, st),
         "gemm_dgrad_glu": lambda: L.call("ffmoe_gemm_dgrad_glu", P(wgo), P(wd), P(up), P(off), P(til),
                                          tr, E, T, D, H, 0, P(gup), gws, st),
-        "gemm_dgrad": lambda: L.call("ffmoe_gemm_dgrad", P(gup), P(wu), P(off), P(til), tr, E, T, H,
-                                     D, P(ghb), gws, st),
+        "gemm_dgrad_wgrad": lambda: L.call("ffmoe_gemm_dgrad_wgrad_shared", P(gup), P(wu), P(xs), P(off),
+                                           P(til), tr, E, T, H, D, P(ghb), P(dwu), None, None, gws, st),
         "gemm_wgrad_down": lambda: L.call("ffmoe_gemm_wgrad", P(wgo), P(act), P(off), E, D, H, P(dwd),
                                           st),
-        "gemm_wgrad_up": lambda: L.call("ffmoe_gemm_wgrad", P(gup), P(xs), P(off), E, 2 * H, D, P(dwu),
-                                        st),
         "route_fwd": lambda: L.call("ffmoe_route_fwd", P(x), P(gate), None, None, N, D, E, k, 0, 0,
                                     P(logits), P(idx), P(tw3), P(lse), P(ws), st),
         "permute": lambda: L.call("ffmoe_permute", P(x), P(idx), P(tw3), P(off), P(counts), N, D, E, k,
@@ -350,8 +351,8 @@ def cpu_baseline(c, sample_tokens, runs=7):
 
 
 # the order traffic_mode launches the hot kernels in (each twice, after a flush)
-TRAFFIC_ORDER = ["gemm_up_down", "gemm_dgrad_glu", "gemm_dgrad", "gemm_wgrad_down",
-                 "gemm_wgrad_up", "route_fwd", "permute", "combine", "route_bwd", "dx_reduce",
+TRAFFIC_ORDER = ["gemm_up_down", "gemm_dgrad_glu", "gemm_dgrad_wgrad", "gemm_wgrad_down",
+                 "route_fwd", "permute", "combine", "route_bwd", "dx_reduce",
                  "gate_grad"]
 CAL_KIB = 256 * 1024  # the calibration copy reads and writes 256 MiB
 
@@ -436,6 +437,8 @@ def algorithmic_bytes(c, rows):
         "gemm_wgrad_down": rows * D * b + rows * H * b + E * D * H * b,
         "gemm_wgrad_up": rows * 2 * H * b + rows * D * b + E * 2 * H * D * b,
     }
+    # the two above: gup read by both
+    out["gemm_dgrad_wgrad"] = out["gemm_dgrad"] + out["gemm_wgrad_up"]
     for name, (w, kind) in algorithmic_work(c, rows).items():
         if kind == "byte" and w is not None:
             out[name] = int(w)
@@ -487,12 +490,18 @@ def traffic_summary(fetch_csv, write_csv, out_path, commands):
         f.write("\n".join(lines))
 
 
-# the grouped-GEMM dispatches of one fwd+bwd step, in launch order: the
-# forward's up + down as one fused launch, or as two where that schedule
-# does not apply
-GEMM_STEP_ORDER = ["gemm_up_down", "gemm_wgrad_down", "gemm_dgrad_glu", "gemm_wgrad_up", "gemm_dgrad"]
-GEMM_STEP_ORDER_UNFUSED = ["gemm_up_glu", "gemm_down", "gemm_wgrad_down", "gemm_dgrad_glu",
-                           "gemm_wgrad_up", "gemm_dgrad"]
+def gemm_step_order(symbols, fwd_only):
+    """The GEMM roles of one step's grouped-GEMM dispatches (kernel symbols
+    in launch order): the forward's up + down as one fused launch or two,
+    the backward's up-side wgrad and dgrad as one fused launch or two."""
+    fused_fwd = bool(symbols) and "updown" in symbols[0]
+    order = ["gemm_up_down"] if fused_fwd else ["gemm_up_glu", "gemm_down"]
+    if fwd_only:
+        return order
+    order += ["gemm_wgrad_down", "gemm_dgrad_glu"]
+    if len(symbols) > len(order) and "gemm_dw" in symbols[len(order)]:
+        return order + ["gemm_dgrad_wgrad"]
+    return order + ["gemm_wgrad_up", "gemm_dgrad"]
 
 
 def stats_summary(prof_dir, bench_log, out_path, title, command):
@@ -516,10 +525,7 @@ def stats_summary(prof_dir, bench_log, out_path, title, command):
     # the grouped GEMMs only (not the dense gate GEMMs or their split-K reduce)
     gemm = [r["Kernel_Name"] for r in trace
             if "ffmoe::gemm_" in r["Kernel_Name"] and "dense" not in r["Kernel_Name"]]
-    fused = bool(gemm) and "updown" in gemm[0]
-    order = GEMM_STEP_ORDER if fused else GEMM_STEP_ORDER_UNFUSED
-    if (line or {}).get("pass") == "fwd":
-        order = order[:1] if fused else order[:2]
+    order = gemm_step_order(gemm, (line or {}).get("pass") == "fwd")
     role_sym = dict(zip(order, gemm[:len(order)]))
     total = sum(float(r["TotalDurationNs"]) for r in stats)
     out = [f"# rocprofv3 kernel statistics: {title}", "",

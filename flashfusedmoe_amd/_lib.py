@@ -46,6 +46,7 @@ SIGNATURES = {
     "ffmoe_gemm_up_glu": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P, _P]),
     "ffmoe_gemm_down": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P]),
     "ffmoe_gemm_up_down_shared": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "ffmoe_gemm_dgrad_wgrad_shared": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P, _P, _P, _P]),
     "ffmoe_gemm_dgrad_glu": (_I, [_P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P]),
     "ffmoe_gemm_dgrad": (_I, [_P, _P, _P, _P, _I, _I, _L, _I, _I, _P, _P, _P]),
     "ffmoe_gemm_wgrad": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),

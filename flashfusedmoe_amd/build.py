@@ -73,6 +73,58 @@ def unsafe_scratch_ops(asm_text):
     return out
 
 
+def unwaited_claim_reads(asm_text):
+    """(kernel, line, instruction) for every path from an assembly-issued
+    returning atomic (`global_atomic_add vN, ..., off sc0`: the fused
+    up+down launch's claims, whose return register the compiler does not
+    know is pending) to an instruction that reads or writes vN, or to the
+    end of the kernel, with no s_waitcnt vmcnt(0) on the way.  Such a read
+    would see the register before the atomic's value arrives (a spill or a
+    copy of it, typically)."""
+    import re
+
+    def vregs(t):
+        out = set()
+        for m in re.finditer(r"\bv\[(\d+):(\d+)\]", t):
+            out |= set(range(int(m.group(1)), int(m.group(2)) + 1))
+        for m in re.finditer(r"\bv(\d+)\b", t):
+            out.add(int(m.group(1)))
+        return out
+
+    bad = []
+    for km in re.finditer(r"^(_Z\S+):", asm_text, re.M):
+        end = asm_text.find(".Lfunc_end", km.start())
+        lines = [ln.split(";")[0].strip() for ln in asm_text[km.start():end].splitlines()]
+        labels = {ln[:-1]: i for i, ln in enumerate(lines) if re.match(r"^\.LBB\d+_\d+:$", ln)}
+        for i, ln in enumerate(lines):
+            m = re.match(r"global_atomic_add v(\d+), .*\boff sc0$", ln)
+            if not m:
+                continue
+            reg, seen, stack = int(m.group(1)), set(), [i + 1]
+            while stack:
+                p = stack.pop()
+                while p < len(lines) and p not in seen:
+                    seen.add(p)
+                    t = lines[p]
+                    if not t or t.endswith(":"):
+                        p += 1
+                        continue
+                    if t.startswith("s_waitcnt") and "vmcnt(0)" in t:
+                        break
+                    if t.startswith("s_endpgm") or (reg in vregs(t) and not t.startswith("s_")):
+                        bad.append((km.group(1), p, t))
+                        break
+                    b = re.match(r"s_cbranch_\w+\s+(\.LBB\d+_\d+)", t)
+                    if b:
+                        stack.append(labels[b.group(1)])
+                    b = re.match(r"s_branch\s+(\.LBB\d+_\d+)", t)
+                    if b:
+                        p = labels[b.group(1)]
+                        continue
+                    p += 1
+    return bad
+
+
 def _compile(unit, objdir):
     src, obj, extra = unit
     obj = os.path.join(objdir, obj)
@@ -90,11 +142,16 @@ def _check_asm(src, objdir):
     if r.returncode != 0:
         raise RuntimeError(f"hipcc -S failed for {src}:\n{r.stderr}")
     with open(out) as f:
-        bad = unsafe_scratch_ops(f.read())
+        text = f.read()
     os.remove(out)
+    bad = unsafe_scratch_ops(text)
     if bad:
         names = sorted({k for k, _, _ in bad})
         raise RuntimeError(f"{src}: register spills inside hand-counted vmcnt sequences in {names}")
+    bad = unwaited_claim_reads(text)
+    if bad:
+        names = sorted({k for k, _, _ in bad})
+        raise RuntimeError(f"{src}: an assembly claim's return register is used before its vmcnt(0) in {names}")
 
 
 def build(verbose=True):

@@ -92,7 +92,7 @@ struct GemmArgs {
 };
 
 // Grouped K: groups of the extra dense group (two when its K is split).
-__device__ __forceinline__ int extra_groups(const GemmArgs& p) {
+__host__ __device__ __forceinline__ int extra_groups(const GemmArgs& p) {
   return p.x_rows > 0 ? (p.x_split > 1 ? 2 : 1) : 0;
 }
 
@@ -1486,6 +1486,110 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
 #endif
 }
 
+// Fused dgrad + up-side wgrad launch: ghb = gup · w_up[e] (grouped rows,
+// BMD x 256 tiles) and dW_up[e] = gupᵀ · x_sorted (grouped K, 256 x 256
+// tiles) read the same gup and are independent, so one persistent grid
+// runs both tile lists as one: the dgrad tiles (the longer ones: K = 2H)
+// first, then the wgrad tiles, groups heaviest first (ties: lower index
+// first).  The list is cut into chunks of G/8 tiles; chunk c belongs to XCD
+// slot c mod 8; a block claims from its own slot (an atomic counter per
+// slot in p.fused's words [0, 8)), then from any slot that still has tiles.
+// No tile waits for another (a wgrad tile of a dense group cut along K
+// waits only for its partner half, which is already running), and no
+// stream-K partials are needed.  Cutting C2's 268 dgrad tiles into K halves
+// as well (so the list's items were of similar length) was slower: 316
+// against 297 us, the halves' fp32 partials cost more than the shorter tail.
+// Claims are made after each tile: issued ahead of it, the claim's return
+// register lived across the tile, and under this kernel's register pressure
+// the compiler spilled it before the value had arrived.
+template <int BMD>
+__global__ __launch_bounds__(kThreads, 1) void gemm_dw_kernel(GemmArgs pd, GemmArgs pw) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
+  constexpr int BW = 256;
+  constexpr int SD = dl_smem_elems<BMD, 256>(), SW = dl_smem_elems<BW, BW>();
+  constexpr int SMAX = SD > SW ? SD : SW;
+  constexpr int kOrd = kLptMaxE + 2;
+  // one LDS variable (see gemm_updown_kernel): the tiles' area, then the
+  // claim words and the wgrad groups' row counts and order
+  __shared__ __attribute__((aligned(1024))) bf16_t sm[SMAX + 2 * (8 + 2 * kOrd)];
+  int* const s_word = reinterpret_cast<int*>(sm + SMAX);
+  int* const s_cnt = s_word + 8;
+  int* const s_ord = s_cnt + kOrd;
+  int* const fl = pd.fused;
+  const int tid = threadIdx.x;
+  const int Rd = ld_const(pd.tile_offsets, pd.E) + extra_tiles<BMD>(pd);
+  const int64_t TD = static_cast<int64_t>(Rd) * pd.n_tiles;
+  const int NG = pw.E + extra_groups(pw);
+  const int per_e = pw.m_tiles * pw.n_tiles;
+  const int64_t TT = TD + static_cast<int64_t>(NG) * per_e;
+  const int S = static_cast<int>(gridDim.x >> 3);
+  for (int i = tid; i < NG; i += kThreads) s_cnt[i] = group_rows(pw, i);
+  __syncthreads();
+  for (int i = tid; i < NG; i += kThreads) {
+    const int ci = s_cnt[i];
+    int rank = 0;
+    for (int j = 0; j < NG; ++j) {
+      const int cj = s_cnt[j];
+      rank += (cj > ci) || (cj == ci && j < i);
+    }
+    s_ord[rank] = i;
+  }
+  __syncthreads();
+  auto list_tile = [&](int j, int x) { return (static_cast<int64_t>(j / S) * 8 + x) * S + j % S; };
+  auto claim = [&](int w) {
+    if (tid == 0) s_word[0] = __hip_atomic_fetch_add(fl + w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int v = s_word[0];
+    __syncthreads();
+    return v;
+  };
+  const int home = static_cast<int>(blockIdx.x & 7);
+  int x = home;
+  int j = claim(x);
+  for (;;) {
+    const int64_t g = list_tile(j, x);
+    if (g >= TT) {
+      if (tid < 64) {
+        const int c = tid < 8 ? __hip_atomic_load(fl + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        const uint32_t m = static_cast<uint32_t>(__ballot(tid < 8 && list_tile(c, tid) < TT)) & 0xFFu;
+        if (tid == 0) {
+          const uint32_t rot = ((m >> (home + 1)) | (m << (7 - home))) & 0xFFu;  // bit i: slot home + 1 + i
+          s_word[1] = rot ? (home + 1 + __builtin_ctz(rot)) & 7 : -1;
+        }
+      }
+      __syncthreads();
+      const int ns = s_word[1];
+      __syncthreads();
+      if (ns < 0) break;
+      x = ns;
+      j = claim(x);
+      continue;
+    }
+    if (g < TD) {
+      const TileCoord tc = decode_rows_tile<BMD, 256>(pd, g, Rd);
+      gemm_dl_tile<BMD, 256, true, false, 0, EPI_STORE, 0, true>(pd, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+    } else {
+      const int64_t u = g - TD;
+      const int r = static_cast<int>(u / per_e);
+      const TileCoord tc =
+          decode_k_tile<BW, BW>(pw, static_cast<int64_t>(s_ord[r]) * per_e + (u - static_cast<int64_t>(r) * per_e));
+      if (tc.extra && pw.x_split > 1)  // one K half of a split dense-group tile
+        gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_CUT, tc.xt,
+                                                                   kPairKey + tc.xt, sm);
+      else
+        gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+    }
+    j = claim(x);
+  }
+  // the last block out has seen every block finish all its tiles: it clears
+  // the claim words for the next launch
+  if (tid == 0) s_word[1] = __hip_atomic_fetch_add(fl + kFusedExit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_word[1] == static_cast<int>(gridDim.x) - 1 && tid < kFusedRow0)
+    __hip_atomic_store(fl + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#endif
+}
+
 // Persistent grouped-rows GEMM, one block per CU.  The R x n_tiles tiles
 // (R = tile_offsets[E], read on the device) are split into whole-tile rounds
 // of G tiles, one per block, and a stream-K tail: the last T - (T/G - 1)*G
@@ -1949,13 +2053,13 @@ extern "C" int ffmoe_gemm_dgrad_glu(const void* wgo, const void* w_down, const v
                                      activation, gup_out, nullptr, sk_workspace, stream);
 }
 
-extern "C" int ffmoe_gemm_dgrad_shared(const void* gup, const void* w_up, const int32_t* offsets,
-                                       const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
-                                       int H, int D, void* ghb_out, const ffmoe_dense_group* shared,
-                                       void* sk_workspace, void* stream) {
+// dgrad arguments: ghb [rows, D] = gup [rows, 2H] · w_up[e] [2H, D], 256-column tiles.
+static int dgrad_args(GemmArgs& a, const void* gup, const void* w_up, const int32_t* offsets,
+                      const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows, int H, int D,
+                      void* ghb_out, const ffmoe_dense_group* shared) {
   if (check_rows("ffmoe_gemm_dgrad", E, max_rows, D, H, tile_rows)) return 1;
-  constexpr int BN = 256;  // 256 x 256 tiles (two stages) under the stream-K schedule
-  GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
+  constexpr int BN = 256;
+  a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (D + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(gup);
   a.B = static_cast<const bf16_t*>(w_up);
   a.C = static_cast<bf16_t*>(ghb_out);
@@ -1965,9 +2069,18 @@ extern "C" int ffmoe_gemm_dgrad_shared(const void* gup, const void* w_up, const 
   a.b_stride = static_cast<int64_t>(2) * H * D;
   a.N = D;
   a.K = 2 * H;
-  if (apply_shared(a, shared, tile_rows, "ffmoe_gemm_dgrad")) return 1;
-  return launch_rows<BN, false, EPI_STORE>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
-                                           "gemm_dgrad");
+  return apply_shared(a, shared, tile_rows, "ffmoe_gemm_dgrad");
+}
+
+extern "C" int ffmoe_gemm_dgrad_shared(const void* gup, const void* w_up, const int32_t* offsets,
+                                       const int32_t* tile_offsets, int tile_rows, int E, int64_t max_rows,
+                                       int H, int D, void* ghb_out, const ffmoe_dense_group* shared,
+                                       void* sk_workspace, void* stream) {
+  GemmArgs a;
+  if (dgrad_args(a, gup, w_up, offsets, tile_offsets, tile_rows, E, max_rows, H, D, ghb_out, shared)) return 1;
+  // 256 x 256 tiles (two stages) under the stream-K schedule
+  return launch_rows<256, false, EPI_STORE>(a, tile_rows, sk_workspace, 0, static_cast<hipStream_t>(stream),
+                                            "gemm_dgrad");
 }
 
 extern "C" int ffmoe_gemm_dgrad(const void* gup, const void* w_up, const int32_t* offsets,
@@ -2099,13 +2212,13 @@ int ffmoe::gate_grad_mfma(const void* gl, const void* x, int64_t N, int D, int E
 #endif
 static int wgrad_lpt(int E) { return E >= FFMOE_WGRAD_LPT_MIN_E && E <= kLptMaxE; }
 
-extern "C" int ffmoe_gemm_wgrad_shared(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
-                                       int Nc, void* c_out, const ffmoe_dense_group* shared, void* sk_workspace,
-                                       void* stream) {
+// wgrad arguments: c[e] [M, Nc] = a[rows of e, M]^T · b[rows of e, Nc], 256 x 256 tiles.
+static int wgrad_args(GemmArgs& a, const void* a_, const void* b_, const int32_t* offsets, int E, int M, int Nc,
+                      void* c_out, const ffmoe_dense_group* shared, void* sk_workspace) {
   if (E < 1 || M <= 0 || M % 8 != 0 || Nc <= 0 || Nc % 8 != 0)
     return set_error("ffmoe_gemm_wgrad: M and Nc must be positive multiples of 8");
   constexpr int BM = 256, BN = 256;
-  GemmArgs a{};
+  a = GemmArgs{};
   a.offsets = offsets;
   a.E = E;
   a.A = static_cast<const bf16_t*>(a_);
@@ -2152,7 +2265,46 @@ extern "C" int ffmoe_gemm_wgrad_shared(const void* a_, const void* b_, const int
     a.total_tiles += static_cast<int64_t>(groups) * P;
     a.lpt = E + groups <= kLptMaxE;
   }
-  return launch<BM, BN, false, false, 1, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_wgrad");
+  return 0;
+}
+
+extern "C" int ffmoe_gemm_wgrad_shared(const void* a_, const void* b_, const int32_t* offsets, int E, int M,
+                                       int Nc, void* c_out, const ffmoe_dense_group* shared, void* sk_workspace,
+                                       void* stream) {
+  GemmArgs a;
+  if (wgrad_args(a, a_, b_, offsets, E, M, Nc, c_out, shared, sk_workspace)) return 1;
+  return launch<256, 256, false, false, 1, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_wgrad");
+}
+
+// The up-side weight gradient and dgrad in one persistent launch where that
+// schedule applies (a workspace, the transpose-read path, 2H a multiple of
+// 64, 128- or 256-row tiles), else the two launches, wgrad first.
+extern "C" int ffmoe_gemm_dgrad_wgrad_shared(const void* gup, const void* w_up, const void* x_sorted,
+                                             const int32_t* offsets, const int32_t* tile_offsets, int tile_rows,
+                                             int E, int64_t max_rows, int H, int D, void* ghb_out, void* dwu_out,
+                                             const ffmoe_dense_group* shared_dgrad,
+                                             const ffmoe_dense_group* shared_wgrad, void* sk_workspace,
+                                             void* stream) {
+  GemmArgs d, w;
+  if (dgrad_args(d, gup, w_up, offsets, tile_offsets, tile_rows, E, max_rows, H, D, ghb_out, shared_dgrad))
+    return 1;
+  if (wgrad_args(w, gup, x_sorted, offsets, E, 2 * H, D, dwu_out, shared_wgrad, sk_workspace)) return 1;
+  const int G = sk_blocks() / 8 * 8;
+  const int NG = E + extra_groups(w);
+  const bool fused = sk_workspace != nullptr && g_use_tr && (2 * H) % DL_BK == 0 && G >= 8 &&
+                     NG <= kLptMaxE + 2 && (tile_rows == 256 || tile_rows == 128);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!fused) {
+    if (launch<256, 256, false, false, 1, EPI_STORE>(w, st, "gemm_wgrad")) return 1;
+    return launch_rows<256, false, EPI_STORE>(d, tile_rows, sk_workspace, 0, st, "gemm_dgrad");
+  }
+  d.fused = reinterpret_cast<int*>(static_cast<char*>(sk_workspace) + fused_words_offset(sk_blocks()));
+  if (tile_rows == 256)
+    hipLaunchKernelGGL(gemm_dw_kernel<256>, dim3(G), dim3(kThreads), 0, st, d, w);
+  else
+    hipLaunchKernelGGL(gemm_dw_kernel<128>, dim3(G), dim3(kThreads), 0, st, d, w);
+  if (check_launch("gemm_dgrad_wgrad")) return 1;
+  return clear_error();
 }
 
 extern "C" int ffmoe_gemm_wgrad(const void* a_, const void* b_, const int32_t* offsets, int E, int M,

@@ -473,15 +473,13 @@ def experts_backward(go: Tensor, x: Tensor, gate: Tensor, w_up: Tensor, w_down: 
     tr = L.gemm_tile_rows(T, E)
     L.call("ffmoe_gemm_dgrad_glu_shared", L.ptr(wgo), L.ptr(w_down), L.ptr(up), L.ptr(offsets),
            L.ptr(tile_offsets), tr, E, T, D, H, activation, L.ptr(gup), _byref(g_dg), ws, st)
-    # the up-projection weight gradient right after the GEMM that wrote `gup`
-    # (128 MiB at C2) while it is still cache-resident; measured ~1% faster
-    # per step than after the dX GEMMs
+    # the up-projection weight gradient and dX's GEMM both read `gup`, right
+    # after the GEMM that wrote it (128 MiB at C2): one persistent launch
+    # where it applies, else the wgrad then the dgrad
     dwu = torch.empty(E, H2, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_wgrad_shared", L.ptr(gup), L.ptr(xs), L.ptr(offsets), E, H2, D, L.ptr(dwu),
-           _byref(g_wu), ws, st)
     ghb = torch.empty(T, D, dtype=_BF16, device=dev)
-    L.call("ffmoe_gemm_dgrad_shared", L.ptr(gup), L.ptr(w_up), L.ptr(offsets), L.ptr(tile_offsets), tr,
-           E, T, H, D, L.ptr(ghb), _byref(g_dx), ws, st)
+    L.call("ffmoe_gemm_dgrad_wgrad_shared", L.ptr(gup), L.ptr(w_up), L.ptr(xs), L.ptr(offsets),
+           L.ptr(tile_offsets), tr, E, T, H, D, L.ptr(ghb), L.ptr(dwu), _byref(g_dx), _byref(g_wu), ws, st)
     dx = torch.empty(N, D, dtype=_BF16, device=dev)
     fused_gate = E <= L.MAX_FUSED_GATE_E
     if fused_gate:  # the gl @ gate term is computed inside the dX reduce

@@ -230,6 +230,21 @@ int ffmoe_gemm_up_down_shared(const void* x_sorted, const void* w_up, const void
                               int E, int64_t max_rows, int D, int H, int activation, void* up_out,
                               void* act_out, void* down_out, const ffmoe_dense_group* shared_up,
                               const ffmoe_dense_group* shared_down, void* sk_workspace, void* stream);
+/* ffmoe_gemm_wgrad_shared(gup, x_sorted, offsets, E, 2H, D, dwu_out,
+ * shared_wgrad, ...) and ffmoe_gemm_dgrad_shared(gup, w_up, ..., ghb_out,
+ * shared_dgrad, ...) as one persistent launch where it applies (a
+ * workspace, 2H a multiple of 64, tile_rows 128 or 256): the two read the
+ * same gup and are independent, so their tiles run as one list, dgrad's
+ * first, with no stream-K partials.  The outputs are those of the two
+ * calls (bit for bit those with sk_workspace NULL, where no tile's K range
+ * is split), which it makes itself where the fused schedule does not
+ * apply.  Replaces: the dX bmm of the up projection and its weight-gradient
+ * bmm (fused_moe.py:553, :565). */
+int ffmoe_gemm_dgrad_wgrad_shared(const void* gup, const void* w_up, const void* x_sorted,
+                                  const int32_t* offsets, const int32_t* tile_offsets, int tile_rows,
+                                  int E, int64_t max_rows, int H, int D, void* ghb_out, void* dwu_out,
+                                  const ffmoe_dense_group* shared_dgrad,
+                                  const ffmoe_dense_group* shared_wgrad, void* sk_workspace, void* stream);
 int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, const void* up,
                                 const int32_t* offsets, const int32_t* tile_offsets,
                                 int tile_rows, int E, int64_t max_rows, int D, int H,

@@ -307,6 +307,81 @@ def test_fused_up_down_matches_two_launches(sizes, D, H, shared_rows, _lib):
         check_close(ref[5], f(ref[4]) @ f(sdn).t(), "shared down")
 
 
+# The fused dgrad + up-side wgrad launch against the two separate launches
+# bit for bit (dgrad with no workspace: whole tiles, as in the fused
+# schedule; the wgrad with the workspace, which cuts a large dense group's K
+# in two either way), with and without a dense group; the last case takes
+# the two-launch path inside the entry point (2H not a multiple of 64).
+@pytest.mark.parametrize("sizes,D,H,shared_rows", [
+    ([2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800], 1024, 2048, 0),
+    ([2048] * 8, 1024, 2048, 8192),
+    ([100 + (37 * e) % 61 for e in range(32)], 512, 256, 0),
+    ([0, 1500, 0, 600], 256, 320, 700),
+    ([700, 900], 256, 104, 0),
+])
+def test_fused_dgrad_wgrad_matches_two_launches(sizes, D, H, shared_rows, _lib):
+    L = _lib
+    E = len(sizes)
+    H2 = 2 * H
+    g = torch.Generator().manual_seed(41 + sum(sizes))
+    T = sum(sizes)
+    bm = L.gemm_tile_rows(T, E)
+    print(f"fused dgrad+wgrad: sizes={sizes[:4]}... E={E} D={D} H={H} shared={shared_rows} tile_rows={bm}",
+          flush=True)
+    off = np.zeros(E + 1, dtype=np.int32)
+    off[1:] = np.cumsum(sizes)
+    tiles = np.zeros(E + 1, dtype=np.int32)
+    tiles[1:] = np.cumsum([-(-s // bm) for s in sizes])
+    gup = torch.randn(T, H2, generator=g).to(torch.bfloat16).cuda()
+    xs = torch.randn(T, D, generator=g).to(torch.bfloat16).cuda()
+    wu = (torch.randn(E, H2, D, generator=g) * D ** -0.5).to(torch.bfloat16).cuda()
+    off_g = torch.from_numpy(off).cuda()
+    til_g = torch.from_numpy(tiles).cuda()
+    st = L.stream_ptr()
+    wsb = L.gemm_workspace(torch.device("cuda"), st)
+    N = shared_rows
+    sgup = torch.randn(N, H2, generator=g).to(torch.bfloat16).cuda()
+    sx = torch.randn(N, D, generator=g).to(torch.bfloat16).cuda()
+    sgu = (torch.randn(H2, D, generator=g) * D ** -0.5).to(torch.bfloat16).cuda()
+
+    def outputs():
+        bf = dict(dtype=torch.bfloat16, device="cuda")
+        o = [torch.empty(T, D, **bf), torch.empty(E, H2, D, **bf), torch.empty(N, D, **bf),
+             torch.empty(H2 if N else 0, D, **bf)]
+        gd = L.dense_group(sgup, sgu, o[2], N, 0) if N else None
+        gw = L.dense_group(sgup, sx, o[3], N, 0) if N else None
+        return o, (ctypes.byref(gd) if gd else None), (ctypes.byref(gw) if gw else None)
+
+    ref, gd, gw = outputs()
+    L.call("ffmoe_gemm_wgrad_shared", gup.data_ptr(), xs.data_ptr(), off_g.data_ptr(), E, H2, D,
+           ref[1].data_ptr(), gw, wsb.data_ptr(), st)
+    L.call("ffmoe_gemm_dgrad_shared", gup.data_ptr(), wu.data_ptr(), off_g.data_ptr(), til_g.data_ptr(), bm,
+           E, T, H, D, ref[0].data_ptr(), gd, None, st)
+    first = None
+    for _ in range(3):
+        got, gd, gw = outputs()
+        L.call("ffmoe_gemm_dgrad_wgrad_shared", gup.data_ptr(), wu.data_ptr(), xs.data_ptr(), off_g.data_ptr(),
+               til_g.data_ptr(), bm, E, T, H, D, got[0].data_ptr(), got[1].data_ptr(), gd, gw, wsb.data_ptr(),
+               st)
+        torch.cuda.synchronize()
+        for name, a, b in zip(["ghb", "dw_up", "shared ghb", "shared dw_up"], got, ref):
+            assert torch.equal(a, b), name
+        first = got
+    assert int(wsb[:8192].view(torch.int32).abs().sum().item()) == 0
+    assert int(wsb[-65536:].view(torch.int32).abs().sum().item()) == 0
+    f = lambda t: t.float()  # noqa: E731
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b > a:
+            check_close(ref[0][a:b], f(gup[a:b]) @ f(wu[e]), f"ghb[e={e}]")
+            check_close(ref[1][e], f(gup[a:b]).t() @ f(xs[a:b]), f"dW_up[e={e}]")
+        else:
+            assert ref[1][e].abs().max().item() == 0
+    if N:
+        check_close(first[2], f(sgup) @ f(sgu), "shared ghb")
+        check_close(ref[3], f(sgup).t() @ f(sx), "shared dW_up")
+
+
 @pytest.mark.parametrize("E", [3, 8, 32])
 def test_dx_reduce_and_gate_grad_against_fp32(E, _lib):
     # dx[n] = bf16(bf16(sum_s ghb[row]) + bf16(gl[n] . gate)); dgate = gl^T x
