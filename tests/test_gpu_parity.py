@@ -382,11 +382,12 @@ def test_fused_dgrad_wgrad_matches_two_launches(sizes, D, H, shared_rows, _lib):
         check_close(ref[3], f(sgup).t() @ f(sx), "shared dW_up")
 
 
+@pytest.mark.parametrize("k", [2, 4, 8, 16])
 @pytest.mark.parametrize("E", [3, 8, 32])
-def test_dx_reduce_and_gate_grad_against_fp32(E, _lib):
+def test_dx_reduce_and_gate_grad_against_fp32(E, k, _lib):
     # dx[n] = bf16(bf16(sum_s ghb[row]) + bf16(gl[n] . gate)); dgate = gl^T x
     L = _lib
-    N, D, k = 1000, 264, 2
+    N, D = 1000, 264
     g = torch.Generator().manual_seed(E)
     T = N * k
     ghb = torch.randn(T, D, generator=g).to(torch.bfloat16)
@@ -415,6 +416,32 @@ def test_dx_reduce_and_gate_grad_against_fp32(E, _lib):
     a = (gl.double() @ gate.double()).to(torch.bfloat16).double()
     check_close(dx.cpu(), (s + a), "dx")
     check_close(dgate.cpu(), gl.double().t() @ x.double(), "dgate")
+
+
+@pytest.mark.parametrize("E", [3, 8, 32])
+def test_dx_reduce_dropped_slots_add_nothing(E, _lib):
+    # The same problem as k = 2 and as k = 16 with slots 2..15 dropped is
+    # the same arithmetic in the same order (dropped slots add nothing), so
+    # the results must be the same bits.
+    L = _lib
+    N, D = 777, 136
+    g = torch.Generator().manual_seed(100 + E)
+    ghb = torch.randn(2 * N, D, generator=g).to(torch.bfloat16).cuda()
+    gl = (torch.randn(N, E, generator=g) * 0.1).to(torch.bfloat16).cuda()
+    gate = (torch.randn(E, D, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    ro2 = torch.randperm(2 * N, generator=g).to(torch.int32)
+    ro2[::29] = L.ROW_DROPPED
+    ro16 = torch.full((N, 16), L.ROW_DROPPED, dtype=torch.int32)
+    ro16[:, :2] = ro2.view(N, 2)
+    st = L.stream_ptr()
+    outs = []
+    for k, ro in ((2, ro2.cuda()), (16, ro16.reshape(-1).cuda())):
+        dx = torch.empty(N, D, dtype=torch.bfloat16, device="cuda")
+        L.call("ffmoe_dx_reduce", ghb.data_ptr(), ro.data_ptr(), gl.data_ptr(), gate.data_ptr(), N, D, E, k,
+               dx.data_ptr(), st)
+        torch.cuda.synchronize()
+        outs.append(dx)
+    assert torch.equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("N,D,E", [(1000, 256, 48), (4096, 1024, 64), (700, 7168, 256), (333, 64, 40)])
