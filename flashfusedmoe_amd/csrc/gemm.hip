@@ -910,13 +910,12 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   // other.  k-step 0 of stage kt+1 is read right after the barrier that
   // publishes it, during k-step 3 of stage kt.
   bf16x8_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
-  // with a transpose-read operand every fragment read is asm (see
-  // lds_read_b128_asm) and lds_frags_ready() does the waiting
-  constexpr bool ASM_READS = !A_KC || !B_KC;
-  auto read_kc = [&](const bf16_t* ptr) {
-    if constexpr (ASM_READS) return lds_read_b128_asm(ptr);
-    else return *reinterpret_cast<const bf16x8_t*>(ptr);
-  };
+  // every fragment read is asm (ds_read_b128 / ds_read_b64_tr_b16) and
+  // lds_frags_ready() does the waiting, one lgkmcnt(0) per fragment set:
+  // with a transpose-read operand the compiler's own waits would count the
+  // untracked asm reads; with two K-contiguous operands its per-fragment
+  // waits were measured slower (C2 up+down 258-260 against 254-255 us)
+  auto read_kc = [&](const bf16_t* ptr) { return lds_read_b128_asm(ptr); };
   auto read_ks = [&](int buf, int ks, bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) {
     const bf16_t* at = smem + buf * STAGE;
     const bf16_t* bt = at + A_EL;
@@ -1020,10 +1019,8 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     read_ks(0, 0, fa0, fb0);
-    // transpose-read operands: wait for a fragment set before its MFMAs
-    auto ready = [&](bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) {
-      if constexpr (!A_KC || !B_KC) lds_frags_ready(fa, fb);
-    };
+    // wait for a fragment set (asm reads) before its MFMAs
+    auto ready = [&](bf16x8_t (&fa)[TM], bf16x8_t (&fb)[TN]) { lds_frags_ready(fa, fb); };
     int cur = 0;  // ring buffer of the stage being computed
     for (int i = 0; i + 1 < nks; ++i) {
       ready(fa0, fb0);
