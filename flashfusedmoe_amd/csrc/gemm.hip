@@ -43,6 +43,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            static_cast<int>(bytes), 0x00020000);
 }
 
+// The same from values the caller knows to be block-uniform, taken from lane
+// 0 so the descriptor is in scalar registers even where the compiler cannot
+// prove them uniform (a descriptor in vector registers turns every buffer
+// instruction into a loop over the distinct values).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_u(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xffffffffu)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32)));
+  const uint32_t n = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(bytes)));
+  return make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo), n);
+}
+
+// buffer-instruction cache policy: non-temporal (streaming)
+constexpr int kNonTemporal = 2;
+// an offset past every descriptor's range: the access is dropped (stores)
+// or returns zeros (loads)
+constexpr uint32_t kOutOfRange = 0xFFFFFFF0u;
+
 static int g_use_tr = 1;  // LDS transpose reads for MN-contiguous operands
 
 struct GemmArgs {
@@ -244,20 +262,20 @@ __device__ __forceinline__ void lds_frags_ready(bf16x8_t (&fa)[NA], bf16x8_t (&f
 // row_base + idx / (BN/8) and columns n0 + (idx % (BN/8))*8 .. +8 of the
 // tile, idx = i * kThreads + tid.  All loads are issued before any store (a
 // vector-memory wait would also drain earlier stores).
-template <int ROWS, int BN>
-constexpr int glu_bwd_items() { return ROWS * (BN / 8) / kThreads; }
+template <int ROWS, int BN, int NT = kThreads>
+constexpr int glu_bwd_items() { return ROWS * (BN / 8) / NT; }
 
-template <int ROWS, int BN>
+template <int ROWS, int BN, int NT = kThreads>
 __device__ __forceinline__ void glu_bwd_prefetch(const GemmArgs& p, int row_base, int row_end, int n0,
                                                  uint4* pg, uint4* pu) {
   constexpr int CH = BN / 8;
-  constexpr int IT = glu_bwd_items<ROWS, BN>();
-  static_assert((ROWS * CH) % kThreads == 0, "whole items");
+  constexpr int IT = glu_bwd_items<ROWS, BN, NT>();
+  static_assert((ROWS * CH) % NT == 0, "whole items");
   const int tid = threadIdx.x;
   const int64_t H = p.H;
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    const int idx = it * kThreads + tid;
+    const int idx = it * NT + tid;
     const int64_t row = static_cast<int64_t>(row_base) + idx / CH;
     const int col = n0 + (idx % CH) * 8;
     pg[it] = make_uint4(0, 0, 0, 0);
@@ -269,107 +287,147 @@ __device__ __forceinline__ void glu_bwd_prefetch(const GemmArgs& p, int row_base
   }
 }
 
-template <int ROWS, int BN, int LDC>
+template <int ROWS, int BN, int LDC, int NT = kThreads>
 __device__ __forceinline__ void glu_bwd_store(const GemmArgs& p, const bf16_t* Cs, int row_base, int row_end,
                                               int n0, const uint4* pg, const uint4* pu) {
   constexpr int CH = BN / 8;
-  constexpr int IT = glu_bwd_items<ROWS, BN>();
+  constexpr int IT = glu_bwd_items<ROWS, BN, NT>();
+  constexpr int BT = IT < 4 ? IT : 4;  // items per batch: a batch's LDS reads go out together
+  static_assert(IT % BT == 0, "whole batches");
   const int tid = threadIdx.x;
   const int64_t H = p.H;
+  // rows past the group fall outside the descriptor's range (dropped)
+  const int rows = max(0, min(row_end - row_base, ROWS));
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc_u(p.C + static_cast<int64_t>(row_base) * 2 * H,
+                                                static_cast<uint32_t>(rows * 2 * H * 2));
   with_act(p.act, [&](auto actc) {
     constexpr int ACT = decltype(actc)::value;
 #pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int idx = it * kThreads + tid;
-      const int ml = idx / CH, c = (idx % CH) * 8;
-      const int64_t row = static_cast<int64_t>(row_base) + ml;
-      const int col = n0 + c;
-      if (row < row_end && col < p.N) {
-        float ga[8], g[8], u[8], gg[8], gu[8];
-        unpack8(*reinterpret_cast<const uint4*>(Cs + ml * LDC + c), ga);
-        unpack8(pg[it], g);
-        unpack8(pu[it], u);
+    for (int b = 0; b < IT; b += BT) {
+      uint4 gav[BT];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) glu_bwd_t<ACT>(ga[i], g[i], u[i], &gg[i], &gu[i]);
-        *reinterpret_cast<uint4*>(p.C + row * 2 * H + col) = pack8(gg);
-        *reinterpret_cast<uint4*>(p.C + row * 2 * H + H + col) = pack8(gu);
+      for (int i = 0; i < BT; ++i) {
+        const int idx = (b + i) * NT + tid;
+        gav[i] = *reinterpret_cast<const uint4*>(Cs + (idx / CH) * LDC + (idx % CH) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < BT; ++i) {
+        const int idx = (b + i) * NT + tid;
+        const int ml = idx / CH, col = n0 + (idx % CH) * 8;
+        float ga[8], g[8], u[8], gg[8], gu[8];
+        unpack8(gav[i], ga);
+        unpack8(pg[b + i], g);
+        unpack8(pu[b + i], u);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) glu_bwd_t<ACT>(ga[k], g[k], u[k], &gg[k], &gu[k]);
+        const uint32_t off = col < p.N ? static_cast<uint32_t>((ml * 2 * H + col) * 2) : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, pack8(gg)), rc, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, pack8(gu)), rc,
+                                               col < p.N ? off + static_cast<uint32_t>(H * 2) : kOutOfRange, 0, 0);
       }
     }
   });
 }
 
 // Stores ROWS rows of a bf16 C tile staged in LDS (row stride LDC) with the
-// block's 256 threads, 16 bytes each: plain store, GLU forward (tile columns
+// block's NT threads, 16 bytes each: plain store, GLU forward (tile columns
 // [0, BN/2) gate, [BN/2, BN) up: writes act and, if requested, the
 // pre-activation) or GLU backward (reads the pre-activation, writes its
 // gradient).  Rows are row_base + i (grouped rows, valid below row_end) or
 // m_base + i (wgrad, valid below M).
-template <int ROWS, int BN, int LDC, int MODE, int EPI, bool CO_C = false>
+template <int ROWS, int BN, int LDC, int MODE, int EPI, bool CO_C = false, int NT = kThreads>
 __device__ __forceinline__ void store_c_tile(const GemmArgs& p, const bf16_t* Cs, int e, int m_base,
                                              int row_base, int row_end, int n0, int a0) {
   const int tid = threadIdx.x;
+  // Every store is a buffer store through a block-uniform descriptor over
+  // the tile's valid rows (rows past them are dropped by its range, columns
+  // past N by an out-of-range offset), so the loops have no branches and
+  // each batch's LDS reads go out before its first store.
   if constexpr (EPI == EPI_GLU_FWD) {
     constexpr int CH = BN / 16;  // 8-column chunks per half row
-    constexpr int IT = ROWS * CH / kThreads;
-    static_assert((ROWS * CH) % kThreads == 0, "whole items");
+    constexpr int IT = ROWS * CH / NT;
+    static_assert((ROWS * CH) % NT == 0, "whole items");
+    constexpr int BT = IT < 4 ? IT : 4;
+    static_assert(IT % BT == 0, "whole batches");
     const int64_t H = p.H;
+    const int rows = max(0, min(row_end - row_base, ROWS));
     // CO_C: the activation rows are read by other blocks of the same launch
-    // (the fused up+down GEMM): device-scope buffer stores (written through
-    // to the level every XCD reads), rows past the group dropped by bounds
+    // (the fused up+down GEMM): device-scope stores (written through to the
+    // level every XCD reads)
     const __amdgpu_buffer_rsrc_t rc =
-        make_rsrc(p.C + static_cast<int64_t>(row_base) * p.ldc,
-                  static_cast<uint32_t>(max(0, min(row_end - row_base, ROWS)) * p.ldc * 2));
+        make_rsrc_u(p.C + static_cast<int64_t>(row_base) * p.ldc, static_cast<uint32_t>(rows * p.ldc * 2));
+    const bool pre = p.C2 != nullptr;
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc_u(pre ? p.C2 + static_cast<int64_t>(row_base) * 2 * H : p.C,
+                    pre ? static_cast<uint32_t>(rows * 2 * H * 2) : 0u);
     with_act(p.act, [&](auto actc) {
       constexpr int ACT = decltype(actc)::value;
-#pragma unroll 4
-      for (int it = 0; it < IT; ++it) {
-        const int idx = it * kThreads + tid;
-        const int ml = idx / CH, c = (idx % CH) * 8;
-        const int64_t row = row_base + ml;
-        const int a = a0 + c;
-        if (row < row_end && a < p.H) {
-          const uint4 gv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
-          const uint4 uv = *reinterpret_cast<const uint4*>(Cs + ml * LDC + BN / 2 + c);
-          float g[8], u[8], o[8];
-          unpack8(gv, g);
-          unpack8(uv, u);
+#pragma unroll 1
+      for (int b = 0; b < IT; b += BT) {
+        uint4 gv[BT], uv[BT];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = glu_fwd_t<ACT>(g[i], u[i]);
-          if (p.C2 != nullptr) {
-            *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + a) = gv;
-            *reinterpret_cast<uint4*>(p.C2 + row * 2 * H + H + a) = uv;
+        for (int i = 0; i < BT; ++i) {
+          const int idx = (b + i) * NT + tid;
+          const bf16_t* src = Cs + (idx / CH) * LDC + (idx % CH) * 8;
+          gv[i] = *reinterpret_cast<const uint4*>(src);
+          uv[i] = *reinterpret_cast<const uint4*>(src + BN / 2);
+        }
+#pragma unroll
+        for (int i = 0; i < BT; ++i) {
+          const int idx = (b + i) * NT + tid;
+          const int ml = idx / CH, a = a0 + (idx % CH) * 8;
+          const bool ok = a < p.H;
+          float g[8], u[8], o[8];
+          unpack8(gv[i], g);
+          unpack8(uv[i], u);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) o[k] = glu_fwd_t<ACT>(g[k], u[k]);
+          if (pre) {
+            const uint32_t po = ok ? static_cast<uint32_t>((ml * 2 * H + a) * 2) : kOutOfRange;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, gv[i]), rp, po, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, uv[i]), rp,
+                                                   ok ? po + static_cast<uint32_t>(H * 2) : kOutOfRange, 0, 0);
           }
-          if constexpr (CO_C)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, pack8(o)), rc,
-                                                   static_cast<uint32_t>((ml * p.ldc + a) * 2), 0, kDeviceScope);
-          else
-            *reinterpret_cast<uint4*>(p.C + row * p.ldc + a) = pack8(o);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4_t, pack8(o)), rc,
+              ok ? static_cast<uint32_t>((ml * p.ldc + a) * 2) : kOutOfRange, 0, CO_C ? kDeviceScope : 0);
         }
       }
     });
   } else if constexpr (EPI == EPI_GLU_BWD) {
-    uint4 pg[glu_bwd_items<ROWS, BN>()], pu[glu_bwd_items<ROWS, BN>()];
-    glu_bwd_prefetch<ROWS, BN>(p, row_base, row_end, n0, pg, pu);
-    glu_bwd_store<ROWS, BN, LDC>(p, Cs, row_base, row_end, n0, pg, pu);
+    uint4 pg[glu_bwd_items<ROWS, BN, NT>()], pu[glu_bwd_items<ROWS, BN, NT>()];
+    glu_bwd_prefetch<ROWS, BN, NT>(p, row_base, row_end, n0, pg, pu);
+    glu_bwd_store<ROWS, BN, LDC, NT>(p, Cs, row_base, row_end, n0, pg, pu);
   } else {
     constexpr int CH = BN / 8;
-    bf16_t* Cb = p.C;
-    if constexpr (MODE == 1) Cb += static_cast<int64_t>(e) * p.c_stride;
-    for (int idx = tid; idx < ROWS * CH; idx += kThreads) {
-      const int ml = idx / CH, c = (idx % CH) * 8;
-      const int64_t row = (MODE == 0) ? static_cast<int64_t>(row_base) + ml : static_cast<int64_t>(m_base) + ml;
-      const bool row_ok = (MODE == 0) ? row < row_end : row < p.M;
-      const int col = n0 + c;
-      if (!row_ok || col >= p.N) continue;
-      if constexpr (MODE == 1) {
-        // weight gradients are not read again by the step: streaming
-        // (non-temporal) stores keep them from evicting the operand rows the
-        // other tiles still read (measured: C5 wgrads -4 to -6%, C2 -2%)
-        __builtin_nontemporal_store(*reinterpret_cast<const f32x4_t*>(Cs + ml * LDC + c),
-                                    reinterpret_cast<f32x4_t*>(Cb + row * p.ldc + col));
-        continue;
+    constexpr int IT = ROWS * CH / NT;
+    static_assert((ROWS * CH) % NT == 0, "whole items");
+    constexpr int BT = IT < 8 ? IT : 8;
+    static_assert(IT % BT == 0, "whole batches");
+    const bf16_t* Cb = (MODE == 1) ? p.C + static_cast<int64_t>(e) * p.c_stride + static_cast<int64_t>(m_base) * p.ldc
+                                   : p.C + static_cast<int64_t>(row_base) * p.ldc;
+    const int rows = (MODE == 1) ? max(0, min(p.M - m_base, ROWS)) : max(0, min(row_end - row_base, ROWS));
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc_u(Cb, static_cast<uint32_t>(rows * p.ldc * 2));
+#pragma unroll 1
+    for (int b = 0; b < IT; b += BT) {
+      uint4 v[BT];
+#pragma unroll
+      for (int i = 0; i < BT; ++i) {
+        const int idx = (b + i) * NT + tid;
+        v[i] = *reinterpret_cast<const uint4*>(Cs + (idx / CH) * LDC + (idx % CH) * 8);
       }
-      *reinterpret_cast<uint4*>(Cb + row * p.ldc + col) = *reinterpret_cast<const uint4*>(Cs + ml * LDC + c);
+#pragma unroll
+      for (int i = 0; i < BT; ++i) {
+        const int idx = (b + i) * NT + tid;
+        const int ml = idx / CH, col = n0 + (idx % CH) * 8;
+        // weight gradients (MODE 1) are not read again by the step:
+        // streaming stores keep them from evicting the operand rows the
+        // other tiles still read (measured: C5 wgrads -4 to -6%, C2 -2%)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4_t, v[i]), rc,
+            col < p.N ? static_cast<uint32_t>((ml * p.ldc + col) * 2) : kOutOfRange, 0,
+            MODE == 1 ? kNonTemporal : 0);
+      }
     }
   }
 }
@@ -753,17 +811,18 @@ constexpr int kSpinLimit = 1 << 22;  // flag polls before a wait gives up
 // counts them complete through the next tile's signal).  XS: the LDS buffer is the caller's (xsm), so that one
 // kernel can run tiles of two shapes out of one allocation.
 constexpr int kCoLoadA = 1, kCoStoreC = 2;
-// signal (fused up+down launch): a counter thread 0 adds 1 to once every
+// signal (fused up+down launch): a counter thread 0 adds signal_add to once every
 // thread has waited for all its earlier vector-memory operations (vmcnt 0)
 // and a block barrier has followed, i.e. once the previous tile's stores are
 // complete; with two stages that is the first K step's wait.
-template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI, int CO = 0, bool XS = false>
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI, int CO = 0, bool XS = false,
+          int NT = kThreads>
 __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord& tc, int k0, int k1,
                                              int role, int slot, int key, bf16_t* xsm = nullptr,
-                                             int* signal = nullptr) {
+                                             int* signal = nullptr, int signal_add = 1) {
   // a tile of the extra dense group reads and writes its own tensors
   GemmArgs p = pa;
-  if (tc.extra) {
+  if (__builtin_amdgcn_readfirstlane(tc.extra ? 1 : 0)) {  // block-uniform: keeps p's pointers scalar
     p.A = pa.xA;
     p.B = pa.xB;
     p.C = pa.xC;
@@ -773,12 +832,15 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
     p.b_stride = 0;
     p.c_stride = 0;
   }
-  constexpr int WM = BM / 2, WN = BN / 2;
+  // NT / 64 waves in a 2 x (NT / 128) grid over the tile
+  static_assert(NT == 256 || NT == 512, "four or eight waves");
+  constexpr int WGN = NT / 128;
+  constexpr int WM = BM / 2, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int A_EL = BM * DL_BK, B_EL = BN * DL_BK;  // elements per stage tile
   constexpr int STAGE = A_EL + B_EL;
-  constexpr int LA = BM * DL_BK / 8 / kThreads;  // 16-byte loads per thread per stage
-  constexpr int LB = BN * DL_BK / 8 / kThreads;
+  constexpr int LA = BM * DL_BK / 8 / NT;  // 16-byte loads per thread per stage
+  constexpr int LB = BN * DL_BK / 8 / NT;
   constexpr int LDC = BN + 8;                // C staging row stride
   constexpr int NS = dl_stages<BM, BN>();
   constexpr int SMEM = dl_smem_elems<BM, BN>();
@@ -806,7 +868,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> (WGN / 2), wn = wave & (WGN - 1);
 
   // buffer descriptors: reads outside [base, base + bytes) return zero
   __amdgpu_buffer_rsrc_t ra, rb;
@@ -827,7 +889,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   uint32_t offa[LA], offb[LB];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
-    const int pos = i * kThreads + tid;
+    const int pos = i * NT + tid;
     if constexpr (A_KC) {
       const int r = pos >> 3, c = (pos & 7) ^ ((r >> 1) & 7);
       offa[i] = static_cast<uint32_t>((r * p.lda + c * 8) * 2);
@@ -838,7 +900,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   }
 #pragma unroll
   for (int i = 0; i < LB; ++i) {
-    const int pos = i * kThreads + tid;
+    const int pos = i * NT + tid;
     if constexpr (B_KC) {
       const int r = pos >> 3, c = (pos & 7) ^ ((r >> 1) & 7);
       int brow;
@@ -876,12 +938,12 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
 #pragma unroll
     for (int i = part * PA; i < (part + 1) * PA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ra, (lds_void_t*)(at + (i * kThreads + wave * 64) * 8), 16,
+          ra, (lds_void_t*)(at + (i * NT + wave * 64) * 8), 16,
           live ? offa[i] + kstep * stepa : 0xFFFFFFF0u, 0, 0, (CO & kCoLoadA) ? kDeviceScope : 0);
 #pragma unroll
     for (int i = part * PB; i < (part + 1) * PB; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (lds_void_t*)(bt + (i * kThreads + wave * 64) * 8), 16,
+          rb, (lds_void_t*)(bt + (i * NT + wave * 64) * 8), 16,
           live ? offb[i] + kstep * stepb : 0xFFFFFFF0u, 0, 0, 0);
   };
   auto issue = [&](int kstep, int buf) {
@@ -981,7 +1043,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   // loads (rows past the group read zeros), so every thread issues exactly
   // 2 * PIT of them, after the last stage load: the wait before the epilogue
   // can then leave them in flight (vector-memory loads complete in order).
-  constexpr int PIT = (EPI == EPI_GLU_BWD) ? glu_bwd_items<BM, BN>() : 1;
+  constexpr int PIT = (EPI == EPI_GLU_BWD) ? glu_bwd_items<BM, BN, NT>() : 1;
   uint4 pre_g[PIT], pre_u[PIT];
   auto prefetch_up = [&]() {
     if constexpr (EPI == EPI_GLU_BWD) {
@@ -989,10 +1051,10 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       const int64_t H2 = 2 * static_cast<int64_t>(p.H);
       const int rows = max(0, min(row_end - row_begin, BM));
       const __amdgpu_buffer_rsrc_t ru =
-          make_rsrc(p.up + static_cast<int64_t>(row_begin) * H2, static_cast<uint32_t>(rows * H2 * 2));
+          make_rsrc_u(p.up + static_cast<int64_t>(row_begin) * H2, static_cast<uint32_t>(rows * H2 * 2));
 #pragma unroll
       for (int it = 0; it < PIT; ++it) {
-        const int idx = it * kThreads + tid;
+        const int idx = it * NT + tid;
         const uint32_t off = static_cast<uint32_t>(((idx / CH) * H2 + n0 + (idx % CH) * 8) * 2);
         pre_g[it] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0));
         pre_u[it] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ru, off + p.H * 2, 0, 0));
@@ -1046,7 +1108,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       asm volatile("" ::: "memory");
       if constexpr (kIn == 0) {
         if (i == 0 && signal != nullptr && tid == 0)
-          __hip_atomic_fetch_add(signal, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(signal, signal_add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       // refill this stage's buffer NS steps ahead (part 0 now, the rest with
       // the next k-steps), read k-step 0 of the next stage, run k-step 3 of
@@ -1086,7 +1148,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   }
   __syncthreads();
   if (signal != nullptr && (kIn != 0 || nks < 2) && tid == 0)
-    __hip_atomic_fetch_add(signal, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(signal, signal_add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   if (role == ROLE_SPLIT) {
     // row r of the tile holds output row row_begin + r (grouped rows) or
@@ -1126,8 +1188,8 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       // completing them (vmcnt 0) is all that must precede the publication;
       // no L2 write-back is needed.  Buffer stores take each store's offset
       // from a scalar constant, so no address registers are kept per store.
-      const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part + static_cast<int64_t>(slot) * NF * kThreads * 4,
-                                                  NF * kThreads * 16);
+      const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part + static_cast<int64_t>(slot) * NF * NT * 4,
+                                                  NF * NT * 16);
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -1137,7 +1199,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
             const f32x4_t v = {acc[tm][tn][4 * q], acc[tm][tn][4 * q + 1], acc[tm][tn][4 * q + 2],
                                acc[tm][tn][4 * q + 3]};
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rp, tid * 16,
-                                                   ((tm * TN + tn) * 4 + q) * kThreads * 16, kDeviceScope);
+                                                   ((tm * TN + tn) * 4 + q) * NT * 16, kDeviceScope);
           }
           __builtin_amdgcn_sched_barrier(0);  // one 32x32 tile of accumulator reads at a time
         }
@@ -1167,7 +1229,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
       *s_word = src - 1;  // -1: no partial to add
     }
     __syncthreads();  // the partial is read below with device-scope loads
-    partner = *s_word;
+    partner = __builtin_amdgcn_readfirstlane(*s_word);  // block-uniform: a scalar descriptor below
     __syncthreads();
   }
 
@@ -1181,8 +1243,8 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   const int lr = lane & 31;
   const int lq = (lane >> 5) * 4;
   const __amdgpu_buffer_rsrc_t rpart =
-      make_rsrc(p.part + static_cast<int64_t>(partner < 0 ? 0 : partner) * NF * kThreads * 4,
-                NF * kThreads * 16);
+      make_rsrc(p.part + static_cast<int64_t>(partner < 0 ? 0 : partner) * NF * NT * 4,
+                NF * NT * 16);
   auto stage = [&](auto add) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
@@ -1196,7 +1258,7 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
           for (int q = 0; q < 4; ++q)
             pv[q] = __builtin_bit_cast(
                 f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                             rpart, tid * 16, ((tm * TN + tn) * 4 + q) * kThreads * 16, kDeviceScope));
+                             rpart, tid * 16, ((tm * TN + tn) * 4 + q) * NT * 16, kDeviceScope));
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             *reinterpret_cast<uint2*>(Cs + ml * LDC + nl + q * 8) =
@@ -1217,9 +1279,9 @@ __device__ __forceinline__ void gemm_dl_tile(const GemmArgs& pa, const TileCoord
   else stage(std::false_type{});
   __syncthreads();
   if constexpr (EPI == EPI_GLU_BWD)
-    glu_bwd_store<BM, BN, LDC>(p, Cs, row_begin, row_end, n0, pre_g, pre_u);
+    glu_bwd_store<BM, BN, LDC, NT>(p, Cs, row_begin, row_end, n0, pre_g, pre_u);
   else
-    store_c_tile<BM, BN, LDC, MODE, EPI, (CO & kCoStoreC) != 0>(p, Cs, e, m0, row_begin, row_end, n0, a0);
+    store_c_tile<BM, BN, LDC, MODE, EPI, (CO & kCoStoreC) != 0, NT>(p, Cs, e, m0, row_begin, row_end, n0, a0);
   __syncthreads();  // the C tile is read before a next tile's loads refill the LDS
 }
 
@@ -1233,7 +1295,7 @@ constexpr int kPairPubOff = 512;
 constexpr int kPairMax = 512;
 
 // Body of the one-block-per-tile kernels.
-template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
+template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI, int NT = kThreads>
 __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   TileCoord tc;
   if constexpr (MODE == 0) {
@@ -1292,9 +1354,9 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
       const int r = sl / c;                                           // rank of the group
       const int sub = static_cast<int>(blockIdx.x & 7) * c + sl % c;  // its tile
       if (r >= NG || sub >= per_e) return;
-      for (int i = threadIdx.x; i < NG; i += kThreads) s_cnt[i] = group_rows(p, i);
+      for (int i = threadIdx.x; i < NG; i += NT) s_cnt[i] = group_rows(p, i);
       __syncthreads();
-      for (int i = threadIdx.x; i < NG; i += kThreads) {
+      for (int i = threadIdx.x; i < NG; i += NT) {
         const int ci = s_cnt[i];
         int rank = 0;
         for (int j = 0; j < NG; ++j) {
@@ -1312,9 +1374,9 @@ __device__ __forceinline__ void gemm_dl_body(const GemmArgs& p) {
   if (!tc.valid) return;
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
   if (MODE == 1 && tc.extra && p.x_split > 1)  // one K half of a split dense-group tile
-    gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_CUT, tc.xt, kPairKey + tc.xt);
+    gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI, 0, false, NT>(p, tc, 0, -1, ROLE_CUT, tc.xt, kPairKey + tc.xt);
   else
-    gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI>(p, tc, 0, -1, ROLE_FULL, 0, 0);
+    gemm_dl_tile<BM, BN, A_KC, B_KC, MODE, EPI, 0, false, NT>(p, tc, 0, -1, ROLE_FULL, 0, 0);
 #endif
 }
 
@@ -1339,7 +1401,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dl2_kernel(GemmArgs p) {
 //   [0, 8)                   up-tile claim counters of the 8 XCD slots
 //   kFusedDown               down-tile claim counter
 //   kFusedExit               blocks that have left
-//   [kFusedRow0, + R)        finished up tiles of each row tile
+//   kFusedHalf               half-tile claim counter (see below)
+//   [kFusedRow0, + R)        finished up tiles of each row tile, in halves
 // Up tiles, in grouped order, are cut into chunks of S = G / 8; chunk c
 // belongs to slot c % 8, so in round k each XCD runs one chunk and the
 // chunks start in tile order.  A block claims up tiles from its own slot
@@ -1349,12 +1412,23 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dl2_kernel(GemmArgs p) {
 // are counted; by then every up tile has been claimed by a running block and
 // up tiles wait for nothing, so the wait ends without any co-residency
 // guarantee (it is bounded all the same: a timeout sets the error word).
+// Staggered start: every block would otherwise reach its up-tile epilogue
+// (192 KiB of stores at 256 x 256) at the same moment as all the others, and
+// the stores of all CUs at once run at the XCDs' write bandwidth.  So the
+// odd blocks of each slot (blockIdx / 8 odd) begin with half of one of the
+// slots' first NH tiles (256 x 128: 64 gate and 64 up columns, claimed from
+// one counter) and take their next tiles half a tile's time after the even
+// blocks; claims of whole tiles start at each slot's tile NH.  Row counts
+// are kept in halves (a whole tile adds 2, a half 1; a row tile is complete
+// at 2 * NU).  Measured at C2 with the odd blocks held back instead: per up
+// tile the store phase 14k -> 9.4k cycles, its next tile's first stage
+// 11k -> 7k.
 // Each claim for the next tile is issued before the current tile, so its
 // latency hides under the tile (it is the oldest vector-memory operation of
 // the tile's waves, which only makes the tile's counted waits stricter).  The act rows cross blocks (and XCDs):
 // up tiles store them with device-scope stores completed before the row
 // count moves, down tiles load them with device-scope loads.
-constexpr int kFusedDown = 8, kFusedExit = 9, kFusedRow0 = 16;
+constexpr int kFusedDown = 8, kFusedExit = 9, kFusedHalf = 10, kFusedRow0 = 16;
 constexpr int kFusedWords = 16384;
 constexpr int64_t kFusedBytes = kFusedWords * 4;
 
@@ -1409,7 +1483,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
   const int home = static_cast<int>(blockIdx.x & 7);
   int x = home;
   int prev_row = -1;  // row tile of this block's last up tile, not yet counted
-  int j = claim(x);
+  int prev_w = 0;     // its weight in the row count: 2 (whole tile) or 1 (half)
+  // Each slot's first NH tiles are done as halves: half item hh (of HT, one
+  // counter) is half hh >> 3 & 1 of tile (hh >> 4) of slot hh & 7.
+  const int NH = (S / 2) / 2;
+  const int HT = 16 * NH;
+  auto half_tile = [&](int hh) {
+    const int64_t t = up_tile(hh >> 4, hh & 7);
+    if (t >= TU) return;
+    int mt, nt;
+    grouped_order(t, R, NU, &mt, &nt);
+    const TileCoord tc = decode_rows_mn<BM, BNU / 2>(pu, mt, 2 * nt + ((hh >> 3) & 1));
+    gemm_dl_tile<BM, BNU / 2, true, true, 0, EPI_GLU_FWD, kCoStoreC, true>(
+        pu, tc, 0, -1, ROLE_FULL, 0, 0, sm, prev_row >= 0 ? fl + kFusedRow0 + prev_row : nullptr, prev_w);
+    prev_row = mt;
+    prev_w = 1;
+  };
+  if ((blockIdx.x >> 3) & 1) {
+    const int hh = claim(kFusedHalf);
+    if (hh < HT) half_tile(hh);
+  }
+  int j = claim(x) + NH;
   for (;;) {
     const int64_t t = up_tile(j, x);
     if (t >= TU) {
@@ -1417,7 +1511,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
       // that is not
       if (tid < 64) {
         const int c = tid < 8 ? __hip_atomic_load(fl + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-        const uint32_t m = static_cast<uint32_t>(__ballot(tid < 8 && up_tile(c, tid) < TU)) & 0xFFu;
+        const uint32_t m = static_cast<uint32_t>(__ballot(tid < 8 && up_tile(c + NH, tid) < TU)) & 0xFFu;
         if (tid == 0) {
           const uint32_t rot = ((m >> (home + 1)) | (m << (7 - home))) & 0xFFu;  // bit i: slot home + 1 + i
           s_word[1] = rot ? (home + 1 + __builtin_ctz(rot)) & 7 : -1;
@@ -1428,10 +1522,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
       __syncthreads();
       if (ns < 0) break;
       x = ns;
-      j = claim(x);
+      j = claim(x) + NH;
       continue;
     }
-    const int nj = claim_ahead(x);
+    const int nj = claim_ahead(x);  // NH is added once the value is in (after the tile)
     int mt, nt;
     grouped_order(t, R, NU, &mt, &nt);
     const TileCoord tc = decode_rows_mn<BM, BNU>(pu, mt, nt);
@@ -1439,24 +1533,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
     // are (during the K loop); it waits for all vector-memory operations
     // (the claim's too) before its epilogue
     gemm_dl_tile<BM, BNU, true, true, 0, EPI_GLU_FWD, kCoStoreC, true>(
-        pu, tc, 0, -1, ROLE_FULL, 0, 0, sm, prev_row >= 0 ? fl + kFusedRow0 + prev_row : nullptr);
+        pu, tc, 0, -1, ROLE_FULL, 0, 0, sm, prev_row >= 0 ? fl + kFusedRow0 + prev_row : nullptr, prev_w);
     prev_row = mt;
+    prev_w = 2;
     if (tid == 0) s_word[0] = nj;
     __syncthreads();
-    j = s_word[0];
+    j = s_word[0] + NH;
     __syncthreads();
   }
+  // no half item is left unclaimed once a block takes down tiles (which wait
+  // for their row tiles), so every wait is for blocks already running
+  for (int hh = claim(kFusedHalf); hh < HT; hh = claim(kFusedHalf)) half_tile(hh);
   // the last up tile's act stores
   wait_vmcnt_le(0);
   __syncthreads();
   if (prev_row >= 0 && tid == 0)
-    __hip_atomic_fetch_add(fl + kFusedRow0 + prev_row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(fl + kFusedRow0 + prev_row, prev_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int d = claim(kFusedDown);
   while (d < TD) {
     const int r = static_cast<int>(d / ND), c = static_cast<int>(d - static_cast<int64_t>(r) * ND);
     if (tid == 0) {
       int polls = 0;
-      while (__hip_atomic_load(fl + kFusedRow0 + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < NU) {
+      while (__hip_atomic_load(fl + kFusedRow0 + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 2 * NU) {
         if (++polls >= kSpinLimit) {  // never expected: the tile is computed from whatever act holds
           __hip_atomic_store(pu.flags + pu.err_idx, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           break;
