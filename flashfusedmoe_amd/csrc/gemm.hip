@@ -1597,12 +1597,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
 // Claims are made after each tile: issued ahead of it, the claim's return
 // register lived across the tile, and under this kernel's register pressure
 // the compiler spilled it before the value had arrived.
+// The list's last NSP wgrad tiles (G/4 of them, at most a quarter of the
+// wgrad tiles) are cut into column halves (256 x 128), so the last round is
+// filled by shorter items: at C2 (268 dgrad tiles of ~200k cycles, 512
+// wgrad tiles of ~113k on 256 CUs) a greedy list schedule puts the busiest
+// CU 24% above the mean with whole tiles and 11% above it with the last 64
+// wgrad tiles halved.
 template <int BMD>
 __global__ __launch_bounds__(kThreads, 1) void gemm_dw_kernel(GemmArgs pd, GemmArgs pw) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
   constexpr int BW = 256;
-  constexpr int SD = dl_smem_elems<BMD, 256>(), SW = dl_smem_elems<BW, BW>();
-  constexpr int SMAX = SD > SW ? SD : SW;
+  constexpr int SD = dl_smem_elems<BMD, 256>(), SW = dl_smem_elems<BW, BW>(), SH = dl_smem_elems<BW, BW / 2>();
+  constexpr int SMAX = SD > SW ? (SD > SH ? SD : SH) : (SW > SH ? SW : SH);
   constexpr int kOrd = kLptMaxE + 2;
   // one LDS variable (see gemm_updown_kernel): the tiles' area, then the
   // claim words and the wgrad groups' row counts and order
@@ -1616,7 +1622,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dw_kernel(GemmArgs pd, GemmA
   const int64_t TD = static_cast<int64_t>(Rd) * pd.n_tiles;
   const int NG = pw.E + extra_groups(pw);
   const int per_e = pw.m_tiles * pw.n_tiles;
-  const int64_t TT = TD + static_cast<int64_t>(NG) * per_e;
+  const int64_t NGT = static_cast<int64_t>(NG) * per_e;  // whole wgrad tiles
+  const int64_t NSP = min(NGT / 4, static_cast<int64_t>(gridDim.x / 4));  // the last ones, halved
+  const int64_t TT = TD + NGT + NSP;
   const int S = static_cast<int>(gridDim.x >> 3);
   for (int i = tid; i < NG; i += kThreads) s_cnt[i] = group_rows(pw, i);
   __syncthreads();
@@ -1664,15 +1672,23 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dw_kernel(GemmArgs pd, GemmA
       const TileCoord tc = decode_rows_tile<BMD, 256>(pd, g, Rd);
       gemm_dl_tile<BMD, 256, true, false, 0, EPI_STORE, 0, true>(pd, tc, 0, -1, ROLE_FULL, 0, 0, sm);
     } else {
-      const int64_t u = g - TD;
+      // wgrad item: whole tile u, or (past NGT - NSP) half (v & 1) of tile
+      // NGT - NSP + v / 2
+      const int64_t u0 = g - TD, v = u0 - (NGT - NSP);
+      const int64_t u = v < 0 ? u0 : NGT - NSP + v / 2;
       const int r = static_cast<int>(u / per_e);
-      const TileCoord tc =
+      TileCoord tc =
           decode_k_tile<BW, BW>(pw, static_cast<int64_t>(s_ord[r]) * per_e + (u - static_cast<int64_t>(r) * per_e));
-      if (tc.extra && pw.x_split > 1)  // one K half of a split dense-group tile
-        gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_CUT, tc.xt,
-                                                                   kPairKey + tc.xt, sm);
-      else
+      if (tc.extra && pw.x_split > 1) {  // one K half of a split dense-group tile (whole in N)
+        if (v < 0 || (v & 1) == 0)
+          gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_CUT, tc.xt,
+                                                                     kPairKey + tc.xt, sm);
+      } else if (v < 0) {
         gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+      } else {
+        tc.n0 += static_cast<int>(v & 1) * (BW / 2);
+        gemm_dl_tile<BW, BW / 2, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+      }
     }
     j = claim(x);
   }
