@@ -1389,19 +1389,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dl_kernel(GemmArgs p) {
   gemm_dl_body<BM, BN, A_KC, B_KC, MODE, EPI>(p);
 }
 
-// 256 x 256 tiles with eight waves (two per SIMD, 128 x 64 each, at most
-// 256 registers a lane): while one wave of a SIMD waits on its loads or LDS
-// reads the other issues MFMAs (K step 3.17 k -> 2.57 k cycles, up GEMM).
+// The same with eight waves (two per SIMD, a 2 x 4 grid of wave tiles, at
+// most 256 registers a lane): while one wave of a SIMD waits on its loads
+// or LDS reads the other issues MFMAs (256 x 256 up GEMM: K step 3.17 k ->
+// 2.57 k cycles).
 template <int BM, int BN, bool A_KC, bool B_KC, int MODE, int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_dl8_kernel(GemmArgs p) {
   gemm_dl_body<BM, BN, A_KC, B_KC, MODE, EPI, 512>(p);
-}
-
-// The same, two blocks per CU (at most 256 registers a lane, 80 KiB of
-// LDS): one block's epilogue runs beside the other's K loop.  Grouped rows.
-template <int BM, int BN, bool A_KC, bool B_KC, int EPI>
-__global__ __launch_bounds__(kThreads, 2) void gemm_dl2_kernel(GemmArgs p) {
-  gemm_dl_body<BM, BN, A_KC, B_KC, 0, EPI>(p);
 }
 
 
@@ -2138,14 +2132,12 @@ extern "C" int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, 
                                            void* sk_workspace, void* stream) {
   if (check_rows("ffmoe_gemm_dgrad_glu", E, max_rows, D, H, tile_rows)) return 1;
   if (activation < 0 || activation > FFMOE_ACT_GEGLU_ERF) return set_error("ffmoe_gemm_dgrad_glu: unknown activation");
-  // 256-row tiles and a short K (= D): 256 x 64 tiles two blocks per CU,
-  // so one block's GLU backward epilogue (VALU work: about a third of a
-  // 256 x 128 tile at K = 1024) overlaps the other's K loop (C2, D 1024:
-  // 142 -> 122 us; C4, D 2048, where the epilogue is a smaller share:
-  // 1.01 -> 1.15 ms, so not there); else 256 x 128 (or 128 x 128) tiles,
-  // a three-stage LDS ring, one block per CU
-  const bool two_per_cu = tile_rows == 256 && g_use_tr && D % DL_BK == 0 && D <= 1024;
-  const int BN = two_per_cu ? 64 : 128;
+  // 256-row tiles: 256 x 128 tiles, a three-stage LDS ring and eight waves,
+  // so one wave of a SIMD runs MFMAs while the other waits on loads (C2:
+  // 120 -> 117.5 us against 256 x 64 tiles two blocks per CU; C4: 0.956 ->
+  // 0.923 ms against four waves); 128-row tiles: the 128 x 128 launches
+  const bool eight = tile_rows == 256 && g_use_tr && D % DL_BK == 0;
+  constexpr int BN = 128;
   GemmArgs a = rows_args(offsets, tile_offsets, E, max_rows, tile_rows, (H + BN - 1) / BN);
   a.A = static_cast<const bf16_t*>(wgo);
   a.B = static_cast<const bf16_t*>(w_down);
@@ -2162,12 +2154,12 @@ extern "C" int ffmoe_gemm_dgrad_glu_shared(const void* wgo, const void* w_down, 
   if (shared != nullptr && shared->rows > 0 && shared->up == nullptr)
     return set_error("ffmoe_gemm_dgrad_glu: the dense extra group needs its pre-activation");
   if (apply_shared(a, shared, tile_rows, "ffmoe_gemm_dgrad_glu")) return 1;
-  if (two_per_cu) {
+  if (eight) {
     if (a.total_tiles <= 0) return clear_error();
     const int64_t grid = (a.total_tiles + 7) / 8 * 8;
     if (grid > 0x7fffffff) return set_error("ffmoe_gemm_dgrad_glu: problem too large");
-    hipLaunchKernelGGL((gemm_dl2_kernel<256, 64, true, false, EPI_GLU_BWD>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL((gemm_dl8_kernel<256, BN, true, false, 0, EPI_GLU_BWD>), dim3(static_cast<unsigned>(grid)),
+                       dim3(512), 0, static_cast<hipStream_t>(stream), a);
     if (check_launch("gemm_dgrad_glu")) return 1;
     return clear_error();
   }
