@@ -246,20 +246,24 @@ def test_persistent_schedule_is_deterministic(sizes, D, H, _lib):
 # workspace: one block per tile, as in the fused schedule, so the outputs are
 # the same bits), with and without a dense group after the routed rows.
 # Cases with 128-row tiles take the two-launch path inside the entry point.
-@pytest.mark.parametrize("sizes,D,H,shared_rows", [
-    ([2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800], 1024, 2048, 0),
-    ([2048] * 8, 1024, 2048, 8192),
-    ([0, 1500, 0, 600], 256, 320, 0),
-    ([700, 900], 256, 64, 513),
-    ([300, 0, 128, 1, 513, 64, 0, 127], 256, 192, 0),
+@pytest.mark.parametrize("sizes,D,H,shared_rows,act", [
+    ([2100, 1900, 2300, 1700, 2048, 2048, 2500, 1800], 1024, 2048, 0, 0),
+    ([2048] * 8, 1024, 2048, 8192, 0),
+    ([0, 1500, 0, 600], 256, 320, 0, 0),
+    ([700, 900], 256, 64, 513, 0),
+    ([300, 0, 128, 1, 513, 64, 0, 127], 256, 192, 0, 0),
+    # the other activations through the same epilogues (whole and half tiles)
+    ([1900, 2200, 2048, 1700], 512, 1024, 1000, 1),
+    ([1900, 2200, 2048, 1700], 512, 1024, 0, 2),
+    ([300, 0, 128, 1, 513, 64, 0, 127], 256, 192, 0, 3),
 ])
-def test_fused_up_down_matches_two_launches(sizes, D, H, shared_rows, _lib):
+def test_fused_up_down_matches_two_launches(sizes, D, H, shared_rows, act, _lib):
     L = _lib
     E = len(sizes)
     xs, wu, wd, off = _groups(E, sizes, D, H, seed=31 + sum(sizes))
     T = xs.shape[0]
     bm = L.gemm_tile_rows(T, E)
-    print(f"fused up+down: sizes={sizes} D={D} H={H} shared={shared_rows} tile_rows={bm}", flush=True)
+    print(f"fused up+down: sizes={sizes} D={D} H={H} shared={shared_rows} act={act} tile_rows={bm}", flush=True)
     tiles = np.zeros(E + 1, dtype=np.int32)
     tiles[1:] = np.cumsum([-(-s // bm) for s in sizes])
     xs_g, wu_g, wd_g = cuda(xs, wu, wd)
@@ -277,19 +281,19 @@ def test_fused_up_down_matches_two_launches(sizes, D, H, shared_rows, _lib):
         bf = dict(dtype=torch.bfloat16, device="cuda")
         o = [torch.empty(T, 2 * H, **bf), torch.empty(T, H, **bf), torch.empty(T, D, **bf),
              torch.empty(N, 2 * H, **bf), torch.empty(N, H, **bf), torch.empty(N, D, **bf)]
-        gu = L.dense_group(sx, sgu, o[4], N, 0, c2=o[3]) if N else None
+        gu = L.dense_group(sx, sgu, o[4], N, act, c2=o[3]) if N else None
         gd = L.dense_group(o[4], sdn, o[5], N, 0) if N else None
         return o, (ctypes.byref(gu) if gu else None), (ctypes.byref(gd) if gd else None)
 
     ref, gu, gd = outputs()
     L.call("ffmoe_gemm_up_glu_shared", xs_g.data_ptr(), wu_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
-           bm, E, T, D, H, 0, ref[0].data_ptr(), ref[1].data_ptr(), gu, None, st)
+           bm, E, T, D, H, act, ref[0].data_ptr(), ref[1].data_ptr(), gu, None, st)
     L.call("ffmoe_gemm_down_shared", ref[1].data_ptr(), wd_g.data_ptr(), off_g.data_ptr(), til_g.data_ptr(),
            bm, E, T, H, D, ref[2].data_ptr(), gd, None, st)
     for _ in range(3):
         got, gu, gd = outputs()
         L.call("ffmoe_gemm_up_down_shared", xs_g.data_ptr(), wu_g.data_ptr(), wd_g.data_ptr(), off_g.data_ptr(),
-               til_g.data_ptr(), bm, E, T, D, H, 0, got[0].data_ptr(), got[1].data_ptr(), got[2].data_ptr(),
+               til_g.data_ptr(), bm, E, T, D, H, act, got[0].data_ptr(), got[1].data_ptr(), got[2].data_ptr(),
                gu, gd, wsb.data_ptr(), st)
         torch.cuda.synchronize()
         for name, a, b in zip(["up", "act", "down", "shared up", "shared act", "shared down"], got, ref):
