@@ -674,10 +674,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 // kt+NS, read stage kt+1's first fragments, then run the last k-step.
 constexpr int DL_BK = 64;
 // Stages of the LDS ring: three where they fit in the 160 KiB of LDS (tiles
-// of at most 384 rows + columns), else two; two for the 64-column tiles,
-// which run two blocks per CU (80 KiB each).
+// of at most 384 rows + columns), else two.
 template <int BM, int BN>
-constexpr int dl_stages() { return BN == 64 ? 2 : ((BM + BN) <= 384 ? 3 : 2); }
+constexpr int dl_stages() { return (BM + BN) <= 384 ? 3 : 2; }
 // LDS elements of a tile: the stage ring, or the C staging tile (rows of
 // BN + 8) the epilogue reuses it for, whichever is larger.
 template <int BM, int BN>
