@@ -1607,8 +1607,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
 // wgrad tiles of ~113k on 256 CUs) a greedy list schedule puts the busiest
 // CU 24% above the mean with whole tiles and 11% above it with the last 64
 // wgrad tiles halved.
-template <int BMD>
-__global__ __launch_bounds__(kThreads, 1) void gemm_dw_kernel(GemmArgs pd, GemmArgs pw) {
+template <int BMD, int NT = kThreads>
+__global__ __launch_bounds__(NT, 1) void gemm_dw_kernel(GemmArgs pd, GemmArgs pw) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass only needs the launch stub
   constexpr int BW = 256;
   constexpr int SD = dl_smem_elems<BMD, 256>(), SW = dl_smem_elems<BW, BW>(), SH = dl_smem_elems<BW, BW / 2>();
@@ -1630,9 +1630,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dw_kernel(GemmArgs pd, GemmA
   const int64_t NSP = min(NGT / 4, static_cast<int64_t>(gridDim.x / 4));  // the last ones, halved
   const int64_t TT = TD + NGT + NSP;
   const int S = static_cast<int>(gridDim.x >> 3);
-  for (int i = tid; i < NG; i += kThreads) s_cnt[i] = group_rows(pw, i);
+  for (int i = tid; i < NG; i += NT) s_cnt[i] = group_rows(pw, i);
   __syncthreads();
-  for (int i = tid; i < NG; i += kThreads) {
+  for (int i = tid; i < NG; i += NT) {
     const int ci = s_cnt[i];
     int rank = 0;
     for (int j = 0; j < NG; ++j) {
@@ -1674,7 +1674,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dw_kernel(GemmArgs pd, GemmA
     }
     if (g < TD) {
       const TileCoord tc = decode_rows_tile<BMD, 256>(pd, g, Rd);
-      gemm_dl_tile<BMD, 256, true, false, 0, EPI_STORE, 0, true>(pd, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+      gemm_dl_tile<BMD, 256, true, false, 0, EPI_STORE, 0, true, NT>(pd, tc, 0, -1, ROLE_FULL, 0, 0, sm);
     } else {
       // wgrad item: whole tile u, or (past NGT - NSP) half (v & 1) of tile
       // NGT - NSP + v / 2
@@ -1685,13 +1685,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dw_kernel(GemmArgs pd, GemmA
           decode_k_tile<BW, BW>(pw, static_cast<int64_t>(s_ord[r]) * per_e + (u - static_cast<int64_t>(r) * per_e));
       if (tc.extra && pw.x_split > 1) {  // one K half of a split dense-group tile (whole in N)
         if (v < 0 || (v & 1) == 0)
-          gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_CUT, tc.xt,
+          gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true, NT>(pw, tc, 0, -1, ROLE_CUT, tc.xt,
                                                                      kPairKey + tc.xt, sm);
       } else if (v < 0) {
-        gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+        gemm_dl_tile<BW, BW, false, false, 1, EPI_STORE, 0, true, NT>(pw, tc, 0, -1, ROLE_FULL, 0, 0, sm);
       } else {
         tc.n0 += static_cast<int>(v & 1) * (BW / 2);
-        gemm_dl_tile<BW, BW / 2, false, false, 1, EPI_STORE, 0, true>(pw, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+        gemm_dl_tile<BW, BW / 2, false, false, 1, EPI_STORE, 0, true, NT>(pw, tc, 0, -1, ROLE_FULL, 0, 0, sm);
       }
     }
     j = claim(x);
@@ -2397,6 +2397,8 @@ extern "C" int ffmoe_gemm_wgrad_shared(const void* a_, const void* b_, const int
   return launch<256, 256, false, false, 1, EPI_STORE>(a, static_cast<hipStream_t>(stream), "gemm_wgrad");
 }
 
+constexpr int kDwEightMaxRows = 512;  // mean rows per expert up to which the fused launch runs eight waves
+
 // The up-side weight gradient and dgrad in one persistent launch where that
 // schedule applies (a workspace, the transpose-read path, 2H a multiple of
 // 64, 128- or 256-row tiles), else the two launches, wgrad first.
@@ -2420,10 +2422,21 @@ extern "C" int ffmoe_gemm_dgrad_wgrad_shared(const void* gup, const void* w_up, 
     return launch_rows<256, false, EPI_STORE>(d, tile_rows, sk_workspace, 0, st, "gemm_dgrad");
   }
   d.fused = reinterpret_cast<int*>(static_cast<char*>(sk_workspace) + fused_words_offset(sk_blocks()));
-  if (tile_rows == 256)
-    hipLaunchKernelGGL(gemm_dw_kernel<256>, dim3(G), dim3(kThreads), 0, st, d, w);
-  else
-    hipLaunchKernelGGL(gemm_dw_kernel<128>, dim3(G), dim3(kThreads), 0, st, d, w);
+  // few rows per expert (short wgrad tiles: K steps of at most 8 on
+  // average): eight waves, which keep more operand loads in flight (C5);
+  // else four (at C2, 2048 rows per expert, eight were slower: 274 -> 281 us)
+  const bool eight = max_rows <= static_cast<int64_t>(kDwEightMaxRows) * E;
+  if (tile_rows == 256) {
+    if (eight)
+      hipLaunchKernelGGL((gemm_dw_kernel<256, 512>), dim3(G), dim3(512), 0, st, d, w);
+    else
+      hipLaunchKernelGGL(gemm_dw_kernel<256>, dim3(G), dim3(kThreads), 0, st, d, w);
+  } else {
+    if (eight)
+      hipLaunchKernelGGL((gemm_dw_kernel<128, 512>), dim3(G), dim3(512), 0, st, d, w);
+    else
+      hipLaunchKernelGGL(gemm_dw_kernel<128>, dim3(G), dim3(kThreads), 0, st, d, w);
+  }
   if (check_launch("gemm_dgrad_wgrad")) return 1;
   return clear_error();
 }
