@@ -322,6 +322,8 @@ def test_fused_up_down_matches_two_launches(sizes, D, H, shared_rows, act, _lib)
     ([100 + (37 * e) % 61 for e in range(32)], 512, 256, 0),
     ([0, 1500, 0, 600], 256, 320, 700),
     ([700, 900], 256, 104, 0),
+    # few rows per expert (the eight-wave launch) with a dense group cut in K
+    ([100 + (37 * e) % 61 for e in range(16)], 512, 256, 5000),
 ])
 def test_fused_dgrad_wgrad_matches_two_launches(sizes, D, H, shared_rows, _lib):
     L = _lib
