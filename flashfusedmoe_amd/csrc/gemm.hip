@@ -1458,7 +1458,8 @@ __global__ __launch_bounds__(512, 1) void gemm_dl8h_kernel(GemmArgs p, int hx) {
 // one counter) and take their next tiles half a tile's time after the even
 // blocks; claims of whole tiles start at each slot's tile NH.  Row counts
 // are kept in halves (a whole tile adds 2, a half 1; a row tile is complete
-// at 2 * NU).  Measured at C2 with the odd blocks held back instead: per up
+// at 2 * NU).  At the other end, the last G/4 down tiles are cut into row
+// halves.  Measured at C2 with the odd blocks held back instead: per up
 // tile the store phase 14k -> 9.4k cycles, its next tile's first stage
 // 11k -> 7k.
 // Each claim for the next tile is issued before the current tile, so its
@@ -1587,9 +1588,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
   __syncthreads();
   if (prev_row >= 0 && tid == 0)
     __hip_atomic_fetch_add(fl + kFusedRow0 + prev_row, prev_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  int d = claim(kFusedDown);
-  while (d < TD) {
-    const int r = static_cast<int>(d / ND), c = static_cast<int>(d - static_cast<int64_t>(r) * ND);
+  // the last NSD = G/4 down tiles are cut into row halves (128 x BND), which
+  // fill the launch's last round with shorter items (C2: 240.5-241.3 ->
+  // 235.6-236.1 us; G/8 the same, G/2 and more slower); claimed after each
+  // tile (a claim issued ahead would be read on paths the build's assembly
+  // check cannot tell apart)
+  const int64_t NSD = min(TD / 4, static_cast<int64_t>(gridDim.x / 4));
+  // waits until row tile r's up tiles are all counted
+  auto wait_row = [&](int r) {
     if (tid == 0) {
       int polls = 0;
       while (__hip_atomic_load(fl + kFusedRow0 + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 2 * NU) {
@@ -1601,6 +1607,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
       }
     }
     __syncthreads();
+  };
+  int d = claim(kFusedDown);
+  while (d < TD - NSD) {
+    const int r = static_cast<int>(d / ND), c = static_cast<int>(d - static_cast<int64_t>(r) * ND);
+    wait_row(r);
     const int nd = claim_ahead(kFusedDown);  // after the wait's loads, which it would join
     const TileCoord tc = decode_rows_mn<BM, BND>(pd, r, c);
     gemm_dl_tile<BM, BND, true, true, 0, EPI_STORE, kCoLoadA, true>(pd, tc, 0, -1, ROLE_FULL, 0, 0, sm);
@@ -1608,6 +1619,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_updown_kernel(GemmArgs pu, G
     __syncthreads();
     d = s_word[0];
     __syncthreads();
+  }
+  while (d < TD + NSD) {
+    const int64_t v = d - (TD - NSD), fd = TD - NSD + v / 2;
+    const int r = static_cast<int>(fd / ND), c = static_cast<int>(fd - static_cast<int64_t>(r) * ND);
+    wait_row(r);
+    TileCoord tc = decode_rows_mn<BM, BND>(pd, r, c);
+    tc.row_begin += static_cast<int>(v & 1) * (BM / 2);
+    if (tc.row_begin < tc.row_end)
+      gemm_dl_tile<BM / 2, BND, true, true, 0, EPI_STORE, kCoLoadA, true>(pd, tc, 0, -1, ROLE_FULL, 0, 0, sm);
+    d = claim(kFusedDown);
   }
   // the last block out has seen every block finish all its tiles: it clears
   // the words for the next launch
