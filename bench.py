@@ -528,7 +528,10 @@ def stats_summary(prof_dir, bench_log, out_path, title, command):
     order = gemm_step_order(gemm, (line or {}).get("pass") == "fwd")
     role_sym = dict(zip(order, gemm[:len(order)]))
     total = sum(float(r["TotalDurationNs"]) for r in stats)
-    out = [f"# rocprofv3 kernel statistics: {title}", "",
+    prefix = "rocprofv3 kernel statistics: "
+    while title.startswith(prefix):  # a title taken from an earlier summary's header
+        title = title[len(prefix):]
+    out = [f"# {prefix}{title}", "",
            "Command (from the repository root on one MI355X):", "", "```", command, "```", "",
            f"Total kernel time: {total / 1e6:.3f} ms over the whole run.", "",
            "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | % of kernel time |",
